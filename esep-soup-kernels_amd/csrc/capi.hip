@@ -1,0 +1,333 @@
+// The extern "C" boundary of libesep_body.so (declared in include/esep_body.h): argument
+// checks, launch-shape selection, dispatch to the kernel templates. No allocation, no
+// synchronization, no global mutable state except the per-thread error message.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include "esep_body.h"
+#include "rmsnorm.hpp"
+#include "rope.hpp"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_fail(hipError_t e, const char* what) {
+  snprintf(g_err, sizeof(g_err), "%s: %s", what, hipGetErrorString(e));
+  return (int)e;
+}
+
+bool float_dt(int dt) { return dt == ESEP_F32 || dt == ESEP_F16 || dt == ESEP_BF16; }
+int dt_bytes(int dt) { return dt == ESEP_F32 || dt == ESEP_I32 ? 4 : (dt == ESEP_I64 ? 8 : 2); }
+bool aligned16(const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15u) == 0; }
+bool ld_ok(int64_t ld, int dt) { return ((ld * dt_bytes(dt)) & 15) == 0; }
+
+// Row-group shape for n columns: the fewest wavefronts per row (wpr) that keep at most three
+// 8-element chunks per lane, and the chunk count per lane for that wpr (at least 2: the
+// smallest instantiated kernel). n <= 16384 gives wpr <= 11.
+void norm_shape(int64_t n, int* wpr, int* nv) {
+  const int64_t chunks = (n + 7) / 8;
+  const int w = (int)((chunks + 3 * 64 - 1) / (3 * 64));
+  const int v = (int)((chunks + 64 * w - 1) / (64 * w));
+  *wpr = w < 1 ? 1 : w;
+  *nv = v < 2 ? 2 : v;
+}
+
+// Groups (rows in flight) per backward block of kBwdThreads threads.
+int bwd_groups(int wpr) { return esep::kBwdThreads / (64 * wpr); }
+
+// LDS bytes of the backward's weight-gradient tree for gpb groups with NV chunks per lane:
+// the most slots any tree level parks at once, each NV * 64 * wpr * 8 floats.
+size_t bwd_tree_lds(int gpb, int nv, int wpr) {
+  int top = 1;
+  while (top < gpb) top <<= 1;
+  int slots = 0;
+  for (int half = top >> 1; half >= 1; half >>= 1) {
+    const int hi = 2 * half < gpb ? 2 * half : gpb;
+    if (hi - half > slots) slots = hi - half;
+  }
+  return (size_t)slots * (size_t)nv * 64 * (size_t)wpr * 8 * sizeof(float);
+}
+
+// Rows-per-block partition of the backward pass with a weight gradient: P blocks of rpb
+// contiguous rows, at most 256 blocks, at least one row per row group. Only (rows, n) enter.
+void bwd_partition(int64_t rows, int64_t n, int64_t* P, int64_t* rpb) {
+  int wpr, nv;
+  norm_shape(n, &wpr, &nv);
+  const int64_t gpb = bwd_groups(wpr);
+  int64_t p = (rows + gpb - 1) / gpb;
+  if (p > 256) p = 256;
+  if (p < 1) p = 1;
+  const int64_t r = (rows + p - 1) / p;
+  *rpb = r;
+  *P = (rows + r - 1) / r;
+}
+
+}  // namespace
+
+extern "C" {
+
+int esep_abi_version(void) { return ESEP_ABI_VERSION; }
+
+const char* esep_last_error(void) { return g_err; }
+
+int esep_rmsnorm_fwd(const void* x, int x_dt, int64_t ld_x, const void* delta, int delta_dt,
+                     int64_t ld_delta, const float* w, void* r_out, int64_t ld_r, void* y, int y_dt,
+                     int64_t ld_y, float* rstd, const int32_t* slot, float* xs, int n_special,
+                     int64_t rows, int64_t n, float eps, void* stream) {
+  g_err[0] = 0;
+  if (n < 1 || n > ESEP_NORM_MAX_COLS)
+    return fail(ESEP_ESHAPE, "rmsnorm_fwd: n=%lld outside [1, %d]", (long long)n, ESEP_NORM_MAX_COLS);
+  if (rows < 0) return fail(ESEP_ESHAPE, "rmsnorm_fwd: rows=%lld < 0", (long long)rows);
+  if (!float_dt(x_dt) || !float_dt(y_dt) || (delta != nullptr && !float_dt(delta_dt)))
+    return fail(ESEP_EINVAL, "rmsnorm_fwd: bad dtype code");
+  if (x == nullptr || y == nullptr || w == nullptr)
+    return fail(ESEP_EINVAL, "rmsnorm_fwd: x, y and w are required");
+  if (n_special < 0 || (n_special > 0 && (slot == nullptr || xs == nullptr)))
+    return fail(ESEP_EINVAL, "rmsnorm_fwd: n_special > 0 needs slot and xs");
+  if (ld_x < n || ld_y < n || (delta && ld_delta < n) || (delta && r_out && ld_r < n))
+    return fail(ESEP_ESHAPE, "rmsnorm_fwd: leading dimension smaller than n");
+  if (rows == 0) return 0;
+
+  esep::FwdArgs a{};
+  a.x = x;
+  a.delta = delta;
+  a.w = w;
+  a.r_out = delta ? r_out : nullptr;
+  a.y = y;
+  a.rstd = rstd;
+  a.slot = slot;
+  a.xs = xs;
+  a.ld_x = ld_x;
+  a.ld_d = ld_delta;
+  a.ld_r = ld_r;
+  a.ld_y = ld_y;
+  a.rows = rows;
+  a.n = (int)n;
+  a.n_special = n_special;
+  a.eps = eps;
+  int wpr, nv;
+  norm_shape(n, &wpr, &nv);
+  a.wpr = wpr;
+  bool vec = (n % 8) == 0 && aligned16(x) && aligned16(y) && aligned16(w) && ld_ok(ld_x, x_dt) &&
+             ld_ok(ld_y, y_dt);
+  if (delta) vec = vec && aligned16(delta) && ld_ok(ld_delta, delta_dt);
+  if (a.r_out) vec = vec && aligned16(r_out) && ld_ok(ld_r, x_dt);
+  if (n_special > 0) vec = vec && aligned16(slot);
+  a.vec = vec ? 1 : 0;
+
+  const int gpb = wpr >= 4 ? 1 : 4 / wpr;
+  const dim3 block(gpb * 64 * wpr);
+  const int64_t blocks = (rows + gpb - 1) / gpb;
+  if (blocks > 0x7fffffff) return fail(ESEP_ESHAPE, "rmsnorm_fwd: too many rows");
+  bool sup = false;
+  const hipError_t e = esep::launch_rmsnorm_fwd(a, x_dt, delta ? delta_dt : -1, y_dt, nv,
+                                                dim3((unsigned)blocks), block,
+                                                static_cast<hipStream_t>(stream), &sup);
+  if (!sup)
+    return fail(ESEP_EINVAL, "rmsnorm_fwd: unsupported dtypes x=%d delta=%d y=%d", x_dt,
+                delta ? delta_dt : -1, y_dt);
+  if (e != hipSuccess) return hip_fail(e, "rmsnorm_fwd launch");
+  return 0;
+}
+
+int64_t esep_rmsnorm_partials(int64_t rows, int64_t n) {
+  if (rows <= 0 || n < 1 || n > ESEP_NORM_MAX_COLS) return 0;
+  int64_t P, rpb;
+  bwd_partition(rows, n, &P, &rpb);
+  return P;
+}
+
+int esep_rmsnorm_bwd(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
+                     const float* dr_out, const void* x, int x_dt, int64_t ld_x, int from_y,
+                     const float* rstd, const float* w, const int32_t* slot, const float* xs,
+                     int n_special, float* dr_f32, void* dx_lp, int dx_dt, int64_t ld_out,
+                     float* dw_partials, int64_t n_partials, void* dw, int dw_dt, int64_t rows,
+                     int64_t n, float eps, void* stream) {
+  g_err[0] = 0;
+  if (n < 1 || n > ESEP_NORM_MAX_COLS)
+    return fail(ESEP_ESHAPE, "rmsnorm_bwd: n=%lld outside [1, %d]", (long long)n, ESEP_NORM_MAX_COLS);
+  if (rows < 0) return fail(ESEP_ESHAPE, "rmsnorm_bwd: rows=%lld < 0", (long long)rows);
+  if (n_dy < 0 || n_dy > ESEP_MAX_DY)
+    return fail(ESEP_EINVAL, "rmsnorm_bwd: n_dy=%d outside [0, %d]", n_dy, ESEP_MAX_DY);
+  if (n_dy > 0 && (dys == nullptr || !float_dt(dy_dt)))
+    return fail(ESEP_EINVAL, "rmsnorm_bwd: dys / dy dtype");
+  for (int i = 0; i < n_dy; ++i)
+    if (dys[i] == nullptr) return fail(ESEP_EINVAL, "rmsnorm_bwd: dys[%d] is NULL", i);
+  if (n_dy > 0 && (x == nullptr || !float_dt(x_dt) || w == nullptr))
+    return fail(ESEP_EINVAL, "rmsnorm_bwd: x, x dtype and w are required");
+  if (from_y && rstd == nullptr)
+    return fail(ESEP_EINVAL, "rmsnorm_bwd: from_y needs the saved rstd");
+  if (n_special < 0 || (n_special > 0 && (!from_y || slot == nullptr || xs == nullptr)))
+    return fail(ESEP_EINVAL, "rmsnorm_bwd: n_special > 0 needs from_y, slot and xs");
+  if (dx_lp != nullptr && !float_dt(dx_dt)) return fail(ESEP_EINVAL, "rmsnorm_bwd: dx dtype");
+  if (dw != nullptr) {
+    if (!float_dt(dw_dt) || dw_partials == nullptr)
+      return fail(ESEP_EINVAL, "rmsnorm_bwd: dw needs dw_partials and a float dtype");
+    const int64_t want = esep_rmsnorm_partials(rows, n);
+    if (rows > 0 && n_partials != want)
+      return fail(ESEP_ESHAPE, "rmsnorm_bwd: n_partials=%lld, this shape needs %lld",
+                  (long long)n_partials, (long long)want);
+  }
+  if ((n_dy > 0 && (ld_dy < n || ld_x < n)) ||
+      ((dr_out || dr_f32 || dx_lp) && ld_out < n))
+    return fail(ESEP_ESHAPE, "rmsnorm_bwd: leading dimension smaller than n");
+  if (rows == 0) return 0;
+
+  esep::BwdArgs a{};
+  for (int i = 0; i < n_dy; ++i) a.dy[i] = dys[i];
+  a.n_dy = n_dy;
+  a.ld_dy = ld_dy;
+  a.dr_out = dr_out;
+  a.x = x;
+  a.ld_x = ld_x;
+  a.from_y = from_y ? 1 : 0;
+  a.rstd = rstd;
+  a.w = w;
+  a.slot = slot;
+  a.xs = xs;
+  a.n_special = n_special;
+  a.dr = dr_f32;
+  a.dx = dx_lp;
+  a.ld_out = ld_out;
+  a.part = dw ? dw_partials : nullptr;
+  a.rows = rows;
+  a.n = (int)n;
+  a.eps = eps;
+  int wpr, nv;
+  norm_shape(n, &wpr, &nv);
+  a.wpr = wpr;
+  const int gpb = bwd_groups(wpr);
+  int64_t blocks;
+  if (dw) {
+    int64_t P, rpb;
+    bwd_partition(rows, n, &P, &rpb);
+    a.rpb = rpb;
+    blocks = P;
+  } else {
+    a.rpb = gpb;
+    blocks = (rows + gpb - 1) / gpb;
+  }
+  if (blocks > 0x7fffffff) return fail(ESEP_ESHAPE, "rmsnorm_bwd: too many rows");
+
+  const int xdt = n_dy > 0 ? x_dt : ESEP_F32;
+  const int dydt = n_dy > 0 ? dy_dt : xdt;
+  const int odt = dx_lp ? dx_dt : ESEP_F32;
+  bool vec = (n % 8) == 0 && aligned16(w);
+  for (int i = 0; i < n_dy; ++i) vec = vec && aligned16(dys[i]);
+  if (n_dy > 0) vec = vec && ld_ok(ld_dy, dy_dt) && aligned16(x) && ld_ok(ld_x, x_dt);
+  if (dr_out) vec = vec && aligned16(dr_out);
+  if (dr_f32) vec = vec && aligned16(dr_f32);
+  if (dx_lp) vec = vec && aligned16(dx_lp) && ld_ok(ld_out, dx_dt);
+  if (dr_out || dr_f32) vec = vec && ld_ok(ld_out, ESEP_F32);
+  if (a.part) vec = vec && aligned16(dw_partials);
+  if (n_special > 0) vec = vec && aligned16(slot);
+  a.vec = vec ? 1 : 0;
+
+  // The element-wise kernel always runs with NV = 3.
+  const size_t lds = dw ? bwd_tree_lds(gpb, vec ? nv : 3, wpr) : 0;
+  bool sup = false;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  hipError_t e = esep::launch_rmsnorm_bwd(a, xdt, dydt, odt, nv, dim3((unsigned)blocks),
+                                          dim3(gpb * 64 * wpr), lds, s, &sup);
+  if (!sup)
+    return fail(ESEP_EINVAL, "rmsnorm_bwd: unsupported dtypes x=%d dy=%d dx=%d", xdt, dydt, odt);
+  if (e != hipSuccess) return hip_fail(e, "rmsnorm_bwd launch");
+  if (dw) {
+    e = esep::launch_dgamma_reduce(dw_partials, blocks, (int)n, dw, dw_dt, s, &sup);
+    if (e != hipSuccess) return hip_fail(e, "rmsnorm_bwd dw reduce launch");
+  }
+  return 0;
+}
+
+int esep_rope(const void* q, const int64_t q_strides[3], const void* q_delta,
+              const int64_t qd_strides[3], const void* k, const int64_t k_strides[3], void* q_out,
+              const int64_t qo_strides[3], void* k_out, const int64_t ko_strides[3], int dt,
+              int64_t B, int64_t S, int HQ, int HK, int D, const void* positions, int pos_dt,
+              const int64_t pos_strides[2], const int32_t* cu_seqlens, int n_seq,
+              const float* inv_freq, float sin_sign, void* stream) {
+  g_err[0] = 0;
+  if (!float_dt(dt)) return fail(ESEP_EINVAL, "rope: bad dtype code %d", dt);
+  if (D != 64 && D != 128 && D != 256) return fail(ESEP_ESHAPE, "rope: D=%d not in {64,128,256}", D);
+  if (B < 0 || S < 0 || HQ < 0 || HK < 0 || HQ + HK < 1)
+    return fail(ESEP_ESHAPE, "rope: bad sizes B=%lld S=%lld HQ=%d HK=%d", (long long)B,
+                (long long)S, HQ, HK);
+  if ((HQ > 0 && (q == nullptr || q_out == nullptr || q_strides == nullptr || qo_strides == nullptr)) ||
+      (HK > 0 && (k == nullptr || k_out == nullptr || k_strides == nullptr || ko_strides == nullptr)))
+    return fail(ESEP_EINVAL, "rope: q/q_out (k/k_out) and their strides are required");
+  if (q_delta != nullptr && (HQ == 0 || qd_strides == nullptr))
+    return fail(ESEP_EINVAL, "rope: q_delta needs q heads and strides");
+  if (inv_freq == nullptr) return fail(ESEP_EINVAL, "rope: inv_freq is required");
+  if (positions != nullptr && cu_seqlens != nullptr)
+    return fail(ESEP_EINVAL, "rope: give positions or cu_seqlens, not both");
+  if (positions != nullptr && ((pos_dt != ESEP_I32 && pos_dt != ESEP_I64) || pos_strides == nullptr))
+    return fail(ESEP_EINVAL, "rope: positions need an int32/int64 dtype and strides");
+  if (cu_seqlens != nullptr && (B != 1 || n_seq < 1))
+    return fail(ESEP_EINVAL, "rope: cu_seqlens needs B == 1 and n_seq >= 1");
+  const int64_t tokens = B * S;
+  if (tokens == 0) return 0;
+  if ((tokens + 3) / 4 > 0x7fffffff) return fail(ESEP_ESHAPE, "rope: too many tokens");
+
+  esep::RopeArgs a{};
+  const int64_t zero[3] = {0, 0, 0};
+  const int64_t* qs = HQ > 0 ? q_strides : zero;
+  const int64_t* qos = HQ > 0 ? qo_strides : zero;
+  const int64_t* ks = HK > 0 ? k_strides : zero;
+  const int64_t* kos = HK > 0 ? ko_strides : zero;
+  const int64_t* qds = q_delta ? qd_strides : zero;
+  for (int i = 0; i < 3; ++i) {
+    a.q_s[i] = qs[i];
+    a.qo_s[i] = qos[i];
+    a.k_s[i] = ks[i];
+    a.ko_s[i] = kos[i];
+    a.qd_s[i] = qds[i];
+  }
+  a.q = q;
+  a.qd = q_delta;
+  a.k = k;
+  a.qo = q_out;
+  a.ko = k_out;
+  a.B = B;
+  a.S = S;
+  a.HQ = HQ;
+  a.HK = HK;
+  a.pos = positions;
+  a.pos_i64 = pos_dt == ESEP_I64 ? 1 : 0;
+  a.pos_s[0] = positions ? pos_strides[0] : 0;
+  a.pos_s[1] = positions ? pos_strides[1] : 0;
+  a.cu = cu_seqlens;
+  a.n_seq = n_seq;
+  a.inv_freq = inv_freq;
+  a.sign = sin_sign;
+  bool vec = true;
+  auto chk = [&](const void* p, const int64_t* st) {
+    if (p == nullptr) return;
+    vec = vec && aligned16(p);
+    for (int i = 0; i < 3; ++i) vec = vec && ld_ok(st[i], dt);
+  };
+  if (HQ > 0) {
+    chk(q, q_strides);
+    chk(q_out, qo_strides);
+    chk(q_delta, qd_strides);
+  }
+  if (HK > 0) {
+    chk(k, k_strides);
+    chk(k_out, ko_strides);
+  }
+  a.vec = vec ? 1 : 0;
+  bool sup = false;
+  const hipError_t e = esep::launch_rope(a, dt, D / 2, static_cast<hipStream_t>(stream), &sup);
+  if (!sup) return fail(ESEP_EINVAL, "rope: unsupported dtype %d / D %d", dt, D);
+  if (e != hipSuccess) return hip_fail(e, "rope launch");
+  return 0;
+}
+
+}  // extern "C"

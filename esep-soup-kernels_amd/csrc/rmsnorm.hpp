@@ -1,0 +1,419 @@
+// RMSNorm forward / backward kernels for gfx950 (MI355X).
+//
+// Mapping. A row of n columns is cut into n/8 chunks of 8 elements. A "row group" of
+// G = 64 * wpr lanes (wpr wavefronts, 1..11) owns one row at a time; lane tg of the group owns
+// chunks tg, tg + G, tg + 2G (NV <= 3 of them), so every load and store is a 16-byte access
+// and a wavefront instruction covers 1 KiB of contiguous 16-bit data. wpr is the smallest
+// count that keeps NV <= 3 (n = 1536: 1 wave, 3 chunks; n = 3584: 3 waves), so a whole row
+// stays in registers between the reduction and the output pass (HBM sees each input once) and
+// the backward's three row arrays (dy, x, dw accumulators) fit the 128 VGPRs that 16
+// wavefronts per CU leave.
+//
+// Reductions: a wavefront sums on DPP (common.hpp, fixed order); groups of several
+// wavefronts add their wave sums through LDS in wave order. Everything is reproducible run
+// to run.
+//
+// Weight gradient (backward): the rows are split into P contiguous blocks of rpb rows, P and
+// rpb depending on (rows, n) only (esep_rmsnorm_partials). Each lane accumulates dy * xhat of
+// its chunks in fp32 registers over the rows its group handles, the groups of a block are
+// combined by a fixed LDS tree, and the block writes one fp32 row of the [P, n] partials.
+// A second kernel sums the partials over P in a fixed order. No atomics anywhere.
+#pragma once
+
+#include <type_traits>
+
+#include "common.hpp"
+
+namespace esep {
+
+struct FwdArgs {
+  const void* x;
+  const void* delta;
+  const float* w;
+  void* r_out;
+  void* y;
+  float* rstd;
+  const int32_t* slot;
+  float* xs;
+  int64_t ld_x, ld_d, ld_r, ld_y;
+  int64_t rows;
+  int n;
+  int n_special;
+  float eps;
+  int wpr;  // wavefronts per row
+  int vec;  // 1: every chunk is a whole 16-byte aligned vector
+};
+
+struct BwdArgs {
+  const void* dy[5];
+  int n_dy;
+  int64_t ld_dy;
+  const float* dr_out;
+  const void* x;
+  int64_t ld_x;
+  int from_y;
+  const float* rstd;  // nullptr: recompute from x
+  const float* w;
+  const int32_t* slot;
+  const float* xs;
+  int n_special;
+  float* dr;    // fp32 [rows, n] or nullptr
+  void* dx;     // low-precision copy or nullptr
+  int64_t ld_out;
+  float* part;  // [P, n] weight-gradient partials or nullptr
+  int64_t rows;
+  int64_t rpb;  // rows per block
+  int n;
+  float eps;
+  int wpr;
+  int vec;
+};
+
+constexpr int kFwdMaxThreads = 1024;
+constexpr int kMaxNV = 3;
+constexpr int kBwdThreads = 1024;
+constexpr int kMaxDy = 5;
+
+// Sum of x over the wavefronts of this row group. `red` holds one float per wavefront.
+__device__ __forceinline__ float row_sum(float x, int wpr, float* red) {
+  x = wave_sum(x);
+  if (wpr == 1) return x;
+  const int wave = wave_id();
+  if ((threadIdx.x & 63) == 0) red[wave] = x;
+  __syncthreads();
+  const int g0 = (wave / wpr) * wpr;
+  float s = red[g0];
+  for (int i = 1; i < wpr; ++i) s += red[g0 + i];
+  __syncthreads();
+  return s;
+}
+
+__device__ __forceinline__ float inv_rms(float ss, int n, float eps) {
+  // mean of squares, then 1 / sqrt(ms + eps): correctly rounded fp32 sqrt and divide.
+  return 1.0f / sqrtf(ss / (float)n + eps);
+}
+
+template <bool VEC, typename T>
+__device__ __forceinline__ void bload(const Span& s, uint32_t off, float (&v)[8]) {
+  Buf<T>::template load<VEC>(s, off, v);
+}
+template <bool VEC, typename T>
+__device__ __forceinline__ void bstore(const Span& s, uint32_t off, const float (&v)[8]) {
+  Buf<T>::template store<VEC>(s, off, v);
+}
+
+// Span of row `row` of a [rows, n] tensor with leading dimension ld (elements); a row that
+// does not exist gets 0 bytes, so its loads read 0 and its stores vanish.
+template <typename T>
+__device__ __forceinline__ Span row_rsrc(const void* base, int64_t row, int64_t ld, int n,
+                                         bool ok) {
+  return make_span(static_cast<const T*>(base) + (ok ? row : 0) * ld,
+                   ok ? (uint32_t)n * (uint32_t)sizeof(T) : 0u);
+}
+
+// ---------------------------------------------------------------------------------------
+// Forward
+// ---------------------------------------------------------------------------------------
+template <int NV, bool VEC, typename TX, typename TD, typename TY>
+__device__ __forceinline__ void fwd_rows(const FwdArgs& a, float* red) {
+  const int G = kWave * a.wpr;
+  const int gpb = blockDim.x / G;
+  const int grp = wave_id() / a.wpr;
+  const int tg = (int)threadIdx.x - grp * G;
+  const int64_t row = (int64_t)blockIdx.x * gpb + grp;
+  const bool ok = row < a.rows;
+  const int n = a.n;
+
+  float v[NV][8];
+  const Span rx = row_rsrc<TX>(a.x, row, a.ld_x, n, ok);
+#pragma unroll
+  for (int k = 0; k < NV; ++k) bload<VEC, TX>(rx, (tg + k * G) * 8 * sizeof(TX), v[k]);
+
+  if constexpr (!std::is_void_v<TD>) {
+    const Span rd = row_rsrc<TD>(a.delta, row, a.ld_d, n, ok);
+    float d[NV][8];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) bload<VEC, TD>(rd, (tg + k * G) * 8 * sizeof(TD), d[k]);
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[k][e] = Elt<TX>::round(v[k][e] + d[k][e]);
+    if (a.r_out != nullptr) {
+      const Span rr = row_rsrc<TX>(a.r_out, row, a.ld_r, n, ok);
+#pragma unroll
+      for (int k = 0; k < NV; ++k) bstore<VEC, TX>(rr, (tg + k * G) * 8 * sizeof(TX), v[k]);
+    }
+  }
+
+  float ss = 0.f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf(v[k][e], v[k][e], ss);
+  ss = row_sum(ss, a.wpr, red);
+  const float inv = inv_rms(ss, n, a.eps);
+
+  const Span rw = make_span(a.w, (uint32_t)n * 4u);
+  const Span ry = row_rsrc<TY>(a.y, row, a.ld_y, n, ok);
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    float w8[8], o[8];
+    bload<VEC, float>(rw, (tg + k * G) * 32, w8);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[e] = w8[e] * (v[k][e] * inv);
+    bstore<VEC, TY>(ry, (tg + k * G) * 8 * sizeof(TY), o);
+  }
+  if (a.rstd != nullptr && ok && tg == 0) a.rstd[row] = inv;
+
+  if (a.n_special > 0 && ok) {
+    const Span rs = make_span(a.slot, (uint32_t)n * 4u);
+    float* xsr = a.xs + row * (int64_t)a.n_special;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      const int col = 8 * (tg + k * G);
+      int s8[8];
+      buf_load8_i32<VEC>(rs, col * 4, s8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        if (col + e < n && s8[e] >= 0) xsr[s8[e]] = v[k][e] * inv;
+    }
+  }
+}
+
+// VEC kernels are instantiated for NV = 2, 3; the element-wise (!VEC) kernel only for
+// NV = 3, which serves every row width (surplus chunks lie past the row and read 0).
+template <int NV, bool VEC, typename TX, typename TD, typename TY>
+__global__ __launch_bounds__(kFwdMaxThreads) void k_rmsnorm_fwd(const FwdArgs a) {
+  __shared__ float red[kFwdMaxThreads / kWave];
+  fwd_rows<NV, VEC, TX, TD, TY>(a, red);
+}
+
+// ---------------------------------------------------------------------------------------
+// Backward
+// ---------------------------------------------------------------------------------------
+template <int NV, bool VEC, typename TX, typename TDY, typename TO>
+__device__ __forceinline__ void bwd_rows(const BwdArgs& a, float* red, float* lds) {
+  const int G = kWave * a.wpr;
+  const int gpb = blockDim.x / G;
+  const int grp = wave_id() / a.wpr;
+  const int tg = (int)threadIdx.x - grp * G;
+  const int n = a.n;
+  const int64_t start = (int64_t)blockIdx.x * a.rpb;
+  const int64_t end = start + a.rpb < a.rows ? start + a.rpb : a.rows;
+  const int iters = (int)((a.rpb + gpb - 1) / gpb);
+  const bool want_dw = a.part != nullptr;
+  const Span rw = make_span(a.w, (uint32_t)n * 4u);
+
+  float acc[NV][8];
+#pragma unroll
+  for (int k = 0; k < NV; ++k)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) acc[k][e] = 0.f;
+
+  for (int it = 0; it < iters; ++it) {
+    const int64_t row = start + grp + (int64_t)it * gpb;
+    const bool ok = row < end;
+    float dr[NV][8];
+
+    if (a.n_dy > 0) {
+      // Everything is updated in place so that three row-sized register arrays are live at
+      // most (acc, dy -> g -> dr, x -> xhat).
+      float dy[NV][8], x[NV][8];
+      {
+        const Span r0 = row_rsrc<TDY>(a.dy[0], row, a.ld_dy, n, ok);
+        const Span rx = row_rsrc<TX>(a.x, row, a.ld_x, n, ok);
+#pragma unroll
+        for (int k = 0; k < NV; ++k) bload<VEC, TDY>(r0, (tg + k * G) * 8 * sizeof(TDY), dy[k]);
+#pragma unroll
+        for (int k = 0; k < NV; ++k) bload<VEC, TX>(rx, (tg + k * G) * 8 * sizeof(TX), x[k]);
+      }
+      // Further consumers' gradients, summed in fp32 (constant indices: no private copy of
+      // the pointer array).
+#pragma unroll
+      for (int i = 1; i < kMaxDy; ++i) {
+        if (i < a.n_dy) {
+          const Span ri = row_rsrc<TDY>(a.dy[i], row, a.ld_dy, n, ok);
+#pragma unroll
+          for (int k = 0; k < NV; ++k) {
+            float t[8];
+            bload<VEC, TDY>(ri, (tg + k * G) * 8 * sizeof(TDY), t);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) dy[k][e] += t[e];
+          }
+        }
+      }
+
+      // rstd: saved, or recomputed from x exactly as the forward computed it.
+      float inv;
+      if (a.rstd == nullptr) {
+        float ss = 0.f;
+#pragma unroll
+        for (int k = 0; k < NV; ++k)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) ss = fmaf(x[k][e], x[k][e], ss);
+        inv = inv_rms(row_sum(ss, a.wpr, red), n, a.eps);
+      } else {
+        inv = ok ? a.rstd[row] : 1.f;
+      }
+
+      // x -> xhat
+      if (a.from_y) {
+        // xhat = y / w for the columns of the row (0 beyond it: no 0 / 0); the exact
+        // channels come from xs.
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+          const int col = 8 * (tg + k * G);
+          float w8[8];
+          bload<VEC, float>(rw, col * 4, w8);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[k][e] = col + e < n ? x[k][e] / w8[e] : 0.f;
+        }
+        if (a.n_special > 0 && ok) {
+          const Span rs = make_span(a.slot, (uint32_t)n * 4u);
+          const float* xsr = a.xs + row * (int64_t)a.n_special;
+#pragma unroll
+          for (int k = 0; k < NV; ++k) {
+            const int col = 8 * (tg + k * G);
+            int s8[8];
+            buf_load8_i32<VEC>(rs, col * 4, s8);
+#pragma unroll
+            for (int e = 0; e < 8; ++e)
+              if (col + e < n && s8[e] >= 0) x[k][e] = xsr[s8[e]];
+          }
+        }
+      } else {
+#pragma unroll
+        for (int k = 0; k < NV; ++k)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) x[k][e] *= inv;
+      }
+
+      if (want_dw && ok) {
+#pragma unroll
+        for (int k = 0; k < NV; ++k)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[k][e] = fmaf(dy[k][e], x[k][e], acc[k][e]);
+      }
+
+      // dy -> g = dy * w; proj = sum g * xhat / n
+      float p = 0.f;
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        float w8[8];
+        bload<VEC, float>(rw, (tg + k * G) * 32, w8);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          dy[k][e] *= w8[e];
+          p = fmaf(dy[k][e], x[k][e], p);
+        }
+      }
+      const float proj = row_sum(p, a.wpr, red) / (float)n;
+
+      // g -> dr = rstd * (g - xhat * proj)
+#pragma unroll
+      for (int k = 0; k < NV; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dr[k][e] = inv * (dy[k][e] - x[k][e] * proj);
+    } else {
+#pragma unroll
+      for (int k = 0; k < NV; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dr[k][e] = 0.f;
+    }
+
+    if (a.dr_out != nullptr) {
+      const Span ro = row_rsrc<float>(a.dr_out, row, a.ld_out, n, ok);
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        float t[8];
+        bload<VEC, float>(ro, (tg + k * G) * 32, t);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dr[k][e] += t[e];
+      }
+    }
+    if (a.dr != nullptr) {
+      const Span ro = row_rsrc<float>(a.dr, row, a.ld_out, n, ok);
+#pragma unroll
+      for (int k = 0; k < NV; ++k) bstore<VEC, float>(ro, (tg + k * G) * 32, dr[k]);
+    }
+    if (a.dx != nullptr) {
+      const Span ro = row_rsrc<TO>(a.dx, row, a.ld_out, n, ok);
+#pragma unroll
+      for (int k = 0; k < NV; ++k) bstore<VEC, TO>(ro, (tg + k * G) * 8 * sizeof(TO), dr[k]);
+    }
+  }
+
+  if (want_dw) {
+    // Fixed tree over the gpb groups of this block: at each level the groups [half, 2 half)
+    // park their accumulators in LDS and the groups below add them. The LDS slot stride is
+    // NV * G * 8 floats, so chunks past the row end stay inside their slot. Group 0 ends with
+    // the block sum and writes it as row blockIdx.x of the partials.
+    const int stride = NV * G * 8;
+    int top = 1;
+    while (top < gpb) top <<= 1;
+    for (int half = top >> 1; half >= 1; half >>= 1) {
+      if (grp >= half && grp < 2 * half && grp < gpb) {
+        float* dst = lds + (grp - half) * stride;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) Chunk<float>::store(dst + 8 * (tg + k * G), acc[k]);
+      }
+      __syncthreads();
+      if (grp < half && grp + half < gpb) {
+        const float* src = lds + grp * stride;
+#pragma unroll
+        for (int k = 0; k < NV; ++k) {
+          float t[8];
+          Chunk<float>::load(src + 8 * (tg + k * G), t);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) acc[k][e] += t[e];
+        }
+      }
+      __syncthreads();
+    }
+    if (grp == 0) {
+      const Span rp = make_span(a.part + (int64_t)blockIdx.x * n, (uint32_t)n * 4u);
+#pragma unroll
+      for (int k = 0; k < NV; ++k) bstore<VEC, float>(rp, (tg + k * G) * 32, acc[k]);
+    }
+  }
+}
+
+template <int NV, bool VEC, typename TX, typename TDY, typename TO>
+__global__ __launch_bounds__(kBwdThreads) void k_rmsnorm_bwd(const BwdArgs a) {
+  __shared__ float red[kBwdThreads / kWave];
+  extern __shared__ float lds[];
+  bwd_rows<NV, VEC, TX, TDY, TO>(a, red, lds);
+}
+
+// Stage 2 of the weight gradient: dw[j] = sum_p part[p, j], p ascending within each of the
+// 16 wavefront strides (p = w, w + 16, ...), then the 16 strided sums in wave order.
+template <typename TW>
+__global__ __launch_bounds__(1024) void k_dgamma_reduce(const float* __restrict__ part,
+                                                          int64_t P, int n, TW* __restrict__ dw) {
+  __shared__ float red[16][64];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int j = blockIdx.x * 64 + lane;
+  float s = 0.f;
+  if (j < n) {
+    for (int64_t p = wave; p < P; p += 16) s += part[p * n + j];
+  }
+  red[wave][lane] = s;
+  __syncthreads();
+  if (wave == 0 && j < n) {
+    float t = red[0][lane];
+#pragma unroll
+    for (int w = 1; w < 16; ++w) t += red[w][lane];
+    dw[j] = Elt<TW>::from_f(t);
+  }
+}
+
+// Launch helpers implemented in the instantiating translation units.
+hipError_t launch_rmsnorm_fwd(const FwdArgs& a, int x_dt, int d_dt, int y_dt, int nv, dim3 grid,
+                              dim3 block, hipStream_t s, bool* supported);
+hipError_t launch_rmsnorm_bwd(const BwdArgs& a, int x_dt, int dy_dt, int o_dt, int nv, dim3 grid,
+                              dim3 block, size_t lds_bytes, hipStream_t s, bool* supported);
+hipError_t launch_dgamma_reduce(const float* part, int64_t P, int n, void* dw, int dw_dt,
+                                hipStream_t s, bool* supported);
+
+}  // namespace esep

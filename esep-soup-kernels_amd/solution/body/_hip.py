@@ -1,0 +1,250 @@
+"""ctypes binding of libesep_body.so, the HIP kernels of the decoder-body path (gfx950).
+
+This module is the only place that talks to the C ABI (include/esep_body.h). It loads the
+library that build.py compiled next to this file, declares every entry point's signature,
+turns a non-zero status into EsepError (with the library's message), and passes torch's
+current HIP stream so that every launch is ordered with the surrounding torch work.
+
+There is no fallback: a missing library, a CPU tensor or an unsupported dtype is an error.
+
+Launch accounting: every entry point records the name of the reference Triton kernel it
+replaces (`_add_rmsnorm_fwd`, `_add_rmsnorm_bwd`, `_rope_kernel`; reference
+solution/body/norm_rope.py:83, :116, :356), so tests can count launches the way the
+reference's tests wrap JITFunction.run (reference solution/test_body_norm_rope.py:200-211).
+"""
+
+import contextlib
+import ctypes
+import threading
+from pathlib import Path
+
+import torch
+
+LIB_PATH = Path(__file__).resolve().with_name("libesep_body.so")
+ABI_VERSION = 1
+
+F32, F16, BF16, I32, I64 = 0, 1, 2, 3, 4
+_DT = {torch.float32: F32, torch.float16: F16, torch.bfloat16: BF16,
+       torch.int32: I32, torch.int64: I64}
+
+# Entry points and their C signatures (include/esep_body.h).
+_vp, _i32, _i64, _f32 = ctypes.c_void_p, ctypes.c_int, ctypes.c_int64, ctypes.c_float
+_I64x3 = ctypes.c_int64 * 3
+_I64x2 = ctypes.c_int64 * 2
+_VP5 = ctypes.c_void_p * 5
+SIGNATURES = {
+    "esep_abi_version": (_i32, []),
+    "esep_last_error": (ctypes.c_char_p, []),
+    "esep_rmsnorm_fwd": (_i32, [_vp, _i32, _i64, _vp, _i32, _i64, _vp, _vp, _i64, _vp, _i32, _i64,
+                                _vp, _vp, _vp, _i32, _i64, _i64, _f32, _vp]),
+    "esep_rmsnorm_partials": (_i64, [_i64, _i64]),
+    "esep_rmsnorm_bwd": (_i32, [_vp, _i32, _i32, _i64, _vp, _vp, _i32, _i64, _i32, _vp, _vp, _vp,
+                                _vp, _i32, _vp, _vp, _i32, _i64, _vp, _i64, _vp, _i32, _i64, _i64,
+                                _f32, _vp]),
+    "esep_rope": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64,
+                         _i32, _i32, _i32, _vp, _i32, _vp, _vp, _i32, _vp, _f32, _vp]),
+}
+
+
+class EsepError(RuntimeError):
+    """A call into libesep_body.so failed (bad argument or launch error)."""
+
+
+_lib = None
+_lock = threading.Lock()
+
+
+def lib():
+    """The loaded library (loaded once, signatures declared). Raises if it is not built."""
+    global _lib
+    if _lib is None:
+        with _lock:
+            if _lib is None:
+                if not LIB_PATH.exists():
+                    raise EsepError(f"{LIB_PATH} is not built: run "
+                                    "`python esep-soup-kernels_amd/build.py` (or __graft_entry__.build())")
+                handle = ctypes.CDLL(str(LIB_PATH))
+                for name, (res, args) in SIGNATURES.items():
+                    fn = getattr(handle, name)
+                    fn.restype, fn.argtypes = res, args
+                got = handle.esep_abi_version()
+                if got != ABI_VERSION:
+                    raise EsepError(f"libesep_body.so ABI {got}, this binding expects {ABI_VERSION}")
+                _lib = handle
+    return _lib
+
+
+# ---------------------------------------------------------------------------------------
+# launch accounting
+# ---------------------------------------------------------------------------------------
+_counters = []
+
+
+def _record(name):
+    for c in _counters:
+        c.append(name)
+
+
+@contextlib.contextmanager
+def count_launches():
+    """Collects the reference kernel names of every library launch made inside the block."""
+    names = []
+    _counters.append(names)
+    try:
+        yield names
+    finally:
+        _counters.remove(names)
+
+
+# ---------------------------------------------------------------------------------------
+# helpers
+# ---------------------------------------------------------------------------------------
+def _check(rc, what):
+    if rc != 0:
+        msg = lib().esep_last_error().decode(errors="replace")
+        raise EsepError(f"{what} failed (status {rc}): {msg}")
+
+
+def dtype_code(dt):
+    try:
+        return _DT[dt]
+    except KeyError:
+        raise EsepError(f"unsupported dtype {dt}") from None
+
+
+def _dev(*tensors):
+    """Device of the first tensor; every given tensor must be a HIP tensor on it."""
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise EsepError(f"libesep_body kernels need device (HIP) tensors, got {t.device}")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise EsepError(f"tensors on different devices: {dev} and {t.device}")
+    return dev
+
+
+def _p(t):
+    return None if t is None else t.data_ptr()
+
+
+def _stream(dev):
+    return torch.cuda.current_stream(dev).cuda_stream
+
+
+def _rows_ld(t, n):
+    """Leading dimension of a [rows, n] tensor whose last dim is contiguous."""
+    if t.dim() != 2 or t.shape[1] != n or (t.shape[0] > 1 and t.stride(1) != 1):
+        raise EsepError(f"expected a [rows, {n}] tensor with unit column stride, got "
+                        f"{tuple(t.shape)} / {t.stride()}")
+    return t.stride(0) if t.shape[0] > 1 else n
+
+
+# ---------------------------------------------------------------------------------------
+# entry points
+# ---------------------------------------------------------------------------------------
+def rmsnorm_fwd(x, w, y, eps, delta=None, r_out=None, rstd=None, slot=None, xs=None,
+                n_special=0, name="_add_rmsnorm_fwd"):
+    """y = w * rmsnorm(x (+ delta)) row-wise; optional r_out, rstd, exact-channel xs.
+    x, delta, r_out, y: [rows, n] (unit column stride); w fp32 [n]; rstd fp32 [rows]."""
+    rows, n = x.shape
+    dev = _dev(x, delta, w, r_out, y, rstd, slot, xs)
+    if w.dtype != torch.float32 or not w.is_contiguous() or w.numel() != n:
+        raise EsepError("w must be a contiguous fp32 [n] tensor")
+    rc = lib().esep_rmsnorm_fwd(
+        _p(x), dtype_code(x.dtype), _rows_ld(x, n),
+        _p(delta), dtype_code(delta.dtype) if delta is not None else 0,
+        _rows_ld(delta, n) if delta is not None else 0,
+        _p(w), _p(r_out), _rows_ld(r_out, n) if r_out is not None else 0,
+        _p(y), dtype_code(y.dtype), _rows_ld(y, n),
+        _p(rstd), _p(slot), _p(xs), int(n_special), rows, n, float(eps), _stream(dev))
+    _check(rc, "esep_rmsnorm_fwd")
+    _record(name)
+
+
+def rmsnorm_partials(rows, n):
+    """Rows of the fp32 weight-gradient workspace esep_rmsnorm_bwd needs for this shape."""
+    return int(lib().esep_rmsnorm_partials(int(rows), int(n)))
+
+
+def rmsnorm_bwd(dys, x, w, eps, from_y=False, rstd=None, dr_out=None, slot=None, xs=None,
+                n_special=0, dr=None, dx=None, dw=None, name="_add_rmsnorm_bwd"):
+    """Backward of rmsnorm_fwd; see esep_rmsnorm_bwd. dys: list of [rows, n] tensors of one
+    dtype (their sum is dy). dr: fp32 [rows, n] out; dx: low-precision [rows, n] out;
+    dw: [n] out (a [P, n] fp32 workspace is allocated here)."""
+    rows, n = x.shape
+    dev = _dev(x, w, rstd, dr_out, slot, xs, dr, dx, dw, *dys)
+    if len(dys) > 5:
+        raise EsepError("at most 5 gradients of y")
+    if w.dtype != torch.float32 or not w.is_contiguous() or w.numel() != n:
+        raise EsepError("w must be a contiguous fp32 [n] tensor")
+    if len({d.dtype for d in dys}) > 1:
+        raise EsepError("all gradients of y must share one dtype")
+    lds = {_rows_ld(d, n) for d in dys}
+    if len(lds) > 1:
+        raise EsepError("all gradients of y must share one row stride")
+    ld_dy = lds.pop() if lds else n
+    outs = [t for t in (dr_out, dr, dx) if t is not None]
+    louts = {_rows_ld(t, n) for t in outs}
+    if len(louts) > 1:
+        raise EsepError("dr_out, dr and dx must share one row stride")
+    ld_out = louts.pop() if louts else n
+    part = None
+    n_part = 0
+    if dw is not None:
+        n_part = rmsnorm_partials(rows, n)
+        part = torch.empty((max(n_part, 1), n), device=dev, dtype=torch.float32)
+    arr = _VP5(*([d.data_ptr() for d in dys] + [None] * (5 - len(dys))))
+    rc = lib().esep_rmsnorm_bwd(
+        arr, len(dys), dtype_code(dys[0].dtype) if dys else 0, ld_dy,
+        _p(dr_out), _p(x), dtype_code(x.dtype), _rows_ld(x, n), int(bool(from_y)),
+        _p(rstd), _p(w), _p(slot), _p(xs), int(n_special),
+        _p(dr), _p(dx), dtype_code(dx.dtype) if dx is not None else 0, ld_out,
+        _p(part), n_part, _p(dw), dtype_code(dw.dtype) if dw is not None else 0,
+        rows, n, float(eps), _stream(dev))
+    _check(rc, "esep_rmsnorm_bwd")
+    _record(name)
+
+
+def rope(q, k, qo, ko, inv_freq, sign, q_delta=None, positions=None, cu_seqlens=None,
+         name="_rope_kernel"):
+    """Rotate q and k (4-D (B, S, H, D) views with unit last stride) into qo / ko.
+    positions: None (pos = s), or an int32/int64 tensor broadcastable as (B, S) given as a
+    (B, S) view; cu_seqlens: int32 [n_seq + 1] (B must be 1)."""
+    dev = _dev(q, k, qo, ko, inv_freq, q_delta, positions, cu_seqlens)
+    B, S, HQ, D = q.shape
+    HK = k.shape[2]
+    for t in (q, k, qo, ko) + ((q_delta,) if q_delta is not None else ()):
+        if t.stride(3) != 1 and t.shape[3] > 1:
+            raise EsepError("rope tensors need a unit stride on the head dim")
+    if inv_freq.dtype != torch.float32 or not inv_freq.is_contiguous() or inv_freq.numel() != D // 2:
+        raise EsepError("inv_freq must be a contiguous fp32 [D/2] tensor")
+    dt = dtype_code(q.dtype)
+    if any(t.dtype != q.dtype for t in (k, qo, ko) + ((q_delta,) if q_delta is not None else ())):
+        raise EsepError("q, k, q_delta and the outputs must share one dtype")
+
+    def st(t):
+        return _I64x3(t.stride(0), t.stride(1), t.stride(2))
+
+    pos_ptr, pos_dt, pos_st = None, 0, None
+    if positions is not None:
+        if positions.dtype not in (torch.int32, torch.int64) or positions.dim() != 2:
+            raise EsepError("positions must be an int32/int64 (B, S) view")
+        pos_ptr, pos_dt = positions.data_ptr(), dtype_code(positions.dtype)
+        pos_st = _I64x2(positions.stride(0) if positions.shape[0] > 1 else 0,
+                        positions.stride(1) if positions.shape[1] > 1 else 0)
+    cu_ptr, n_seq = None, 0
+    if cu_seqlens is not None:
+        if cu_seqlens.dtype != torch.int32 or cu_seqlens.dim() != 1 or not cu_seqlens.is_contiguous():
+            raise EsepError("cu_seqlens must be a contiguous int32 [n_seq + 1] tensor")
+        cu_ptr, n_seq = cu_seqlens.data_ptr(), cu_seqlens.numel() - 1
+    rc = lib().esep_rope(
+        q.data_ptr(), st(q), _p(q_delta), st(q_delta) if q_delta is not None else None,
+        k.data_ptr(), st(k), qo.data_ptr(), st(qo), ko.data_ptr(), st(ko),
+        dt, B, S, HQ, HK, D, pos_ptr, pos_dt, pos_st, cu_ptr, n_seq,
+        inv_freq.data_ptr(), float(sign), _stream(dev))
+    _check(rc, "esep_rope")
+    _record(name)

@@ -1,0 +1,164 @@
+/*
+ * esep_body.h — C ABI of libesep_body.so: the decoder-body RMSNorm and rotary-embedding
+ * kernels (forward and backward) for AMD Instinct MI355X (gfx950).
+ *
+ * The reference implementation of this path is a set of Triton kernels launched from Python
+ * (gojosatorukz/esep-soup-kernels, solution/body/norm_rope.py). Each entry point below replaces
+ * one launch site of that file; the citation on each declaration names it. The Python layer
+ * (solution/body/norm_rope.py in this repository) keeps the reference's public API and calls
+ * these functions through ctypes.
+ *
+ * Conventions
+ *  - Every pointer is a device pointer unless stated otherwise. The library never allocates,
+ *    frees or synchronizes: the caller owns every buffer, including workspaces.
+ *  - Work is enqueued asynchronously on `stream` (a hipStream_t passed as void*; NULL is the
+ *    default stream).
+ *  - Return value: 0 on success; a negative ESEP_E* code for a rejected argument (nothing was
+ *    launched); a positive hipError_t if a launch failed. esep_last_error() returns a message for
+ *    the last failure on the calling thread.
+ *  - Strides and leading dimensions are in elements, not bytes. The innermost dimension is
+ *    always contiguous (stride 1).
+ *  - Element types are the esep_dtype codes below.
+ */
+#ifndef ESEP_BODY_H
+#define ESEP_BODY_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ESEP_ABI_VERSION 1
+
+/* Element type codes. */
+enum esep_dtype {
+  ESEP_F32 = 0,
+  ESEP_F16 = 1,
+  ESEP_BF16 = 2,
+  ESEP_I32 = 3,
+  ESEP_I64 = 4
+};
+
+/* Error codes (negative returns). */
+enum esep_status {
+  ESEP_OK = 0,
+  ESEP_EINVAL = -1,   /* bad pointer / dtype / flag combination */
+  ESEP_ESHAPE = -2,   /* unsupported or inconsistent size */
+  ESEP_EALIGN = -3    /* reserved: alignment cannot be served */
+};
+
+/* Widest row the RMSNorm kernels accept (columns). The reference caps rows at
+ * NORM_BLOCK = 2048 (solution/body/norm_rope.py:73, :215). */
+#define ESEP_NORM_MAX_COLS 16384
+
+/* Most gradients of one norm output summed by the backward kernel. Reference: MAX_DY
+ * (solution/body/norm_rope.py:113). */
+#define ESEP_MAX_DY 5
+
+/* ABI version of the loaded library (ESEP_ABI_VERSION at build time). */
+int esep_abi_version(void);
+
+/* Message of the last failed call on this thread ("" if none). Valid until the next call. */
+const char* esep_last_error(void);
+
+/*
+ * RMSNorm forward with optional fused residual add.
+ * Replaces the launch of _add_rmsnorm_fwd at solution/body/norm_rope.py:232-236 (AddRMSNorm.forward)
+ * and :321-322 (rmsnorm_recompute); kernel math follows norm_rope.py:83-109.
+ *
+ *   r      = x (+ delta)                 fp32 math; if r_out != NULL it is stored in x's dtype,
+ *                                         and for a 16-bit x the stored (rounded) r is normalized
+ *   rstd_t = 1 / sqrt(mean_j r_tj^2 + eps)
+ *   y_tj   = w_j * (r_tj * rstd_t)        stored as y_dt
+ *   xs[t, slot[j]] = r_tj * rstd_t        for slot[j] >= 0, when n_special > 0
+ *
+ * x [rows, n] (x_dt), row stride ld_x; delta [rows, n] (delta_dt) or NULL, stride ld_delta;
+ * w [n] fp32; r_out [rows, n] (x_dt) or NULL, stride ld_r (ignored without delta);
+ * y [rows, n] (y_dt), stride ld_y; rstd [rows] fp32 or NULL; slot [n] int32 or NULL;
+ * xs [rows, n_special] fp32 (contiguous) or NULL.
+ * Requires 1 <= n <= ESEP_NORM_MAX_COLS; rows >= 0 (rows == 0 launches nothing).
+ */
+int esep_rmsnorm_fwd(const void* x, int x_dt, int64_t ld_x,
+                     const void* delta, int delta_dt, int64_t ld_delta,
+                     const float* w,
+                     void* r_out, int64_t ld_r,
+                     void* y, int y_dt, int64_t ld_y,
+                     float* rstd,
+                     const int32_t* slot, float* xs, int n_special,
+                     int64_t rows, int64_t n, float eps, void* stream);
+
+/*
+ * Number of rows of the fp32 [P, n] weight-gradient workspace that esep_rmsnorm_bwd needs for
+ * this shape. Depends only on (rows, n), never on the device, so the two-stage dw reduction
+ * is bitwise reproducible. No reference counterpart (the reference computes no weight
+ * gradient: norm_rope.py:286 returns None for it).
+ */
+int64_t esep_rmsnorm_partials(int64_t rows, int64_t n);
+
+/*
+ * RMSNorm backward (dx, and optionally the weight gradient).
+ * Replaces the launch of _add_rmsnorm_bwd at solution/body/norm_rope.py:279-283
+ * (AddRMSNorm.backward); kernel math follows norm_rope.py:116-162.
+ *
+ *   dy     = sum_{i < n_dy} dys[i]            fp32 registers (dys[i] [rows, n] dy_dt, stride ld_dy)
+ *   xhat   = x * rstd                          (from_y == 0; x is the normalized input r)
+ *          = x / w, xs[t, slot[j]] where slot[j] >= 0   (from_y == 1; x is the saved output y)
+ *   rstd   = saved rstd[t], or recomputed from x when rstd == NULL (from_y == 0 only)
+ *   g      = dy * w;  proj = sum_j g * xhat / n
+ *   dr     = rstd * (g - xhat * proj) (+ dr_out)         (dr_out fp32 [rows, n] or NULL)
+ *   dr_f32 [rows, n] fp32 or NULL  <- dr
+ *   dx_lp  [rows, n] dx_dt or NULL <- dr rounded to dx_dt
+ *   dw_j   = sum_t dy_tj * xhat_tj             when dw != NULL: stage 1 writes the
+ *            partials [P, n] fp32 (P = esep_rmsnorm_partials(rows, n), n_partials must equal P),
+ *            stage 2 sums them in a fixed order into dw [n] (dw_dt)
+ * n_dy == 0 and dr_out != NULL gives dr = dr_out. Contiguous rows for dr_out, dr_f32, dx_lp
+ * use ld_out; x uses ld_x.
+ */
+int esep_rmsnorm_bwd(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
+                     const float* dr_out,
+                     const void* x, int x_dt, int64_t ld_x, int from_y,
+                     const float* rstd,
+                     const float* w,
+                     const int32_t* slot, const float* xs, int n_special,
+                     float* dr_f32, void* dx_lp, int dx_dt, int64_t ld_out,
+                     float* dw_partials, int64_t n_partials, void* dw, int dw_dt,
+                     int64_t rows, int64_t n, float eps, void* stream);
+
+/*
+ * Rotary embedding on q and k in one launch (forward with sin_sign = +1, backward with -1).
+ * Replaces the launch of _rope_kernel at solution/body/norm_rope.py:388-392 (_launch_rope);
+ * kernel math follows norm_rope.py:330-369 (rotate_half convention of HF apply_rotary_pos_emb).
+ *
+ * Tokens are indexed (b, s) with b < B, s < S. Element (b, s, h, d) of a tensor X lives at
+ * X + b*X_strides[0] + s*X_strides[1] + h*X_strides[2] + d. The packed reference layout
+ * [T, H, D] is B = 1, S = T; HF's [B, H, S, D] view is any permutation of strides.
+ *
+ *   angle_j = float(pos) * inv_freq[j]          one fp32 multiply, j < D/2
+ *   c = cos(angle), s = sin_sign * sin(angle)   computed in registers (no cos/sin table)
+ *   x = q (+ q_delta, added in the storage dtype) | k
+ *   out[:D/2] = x1*c - x2*s,  out[D/2:] = x2*c + x1*s
+ *
+ * Position source (exactly one):
+ *   positions != NULL: pos = positions[b*pos_strides[0] + s*pos_strides[1]] (pos_dt I32/I64);
+ *   cu_seqlens != NULL (B must be 1): pos = s - cu_seqlens[i] for cu_seqlens[i] <= s <
+ *     cu_seqlens[i+1], i < n_seq (int32, cu_seqlens[0] == 0, cu_seqlens[n_seq] == S);
+ *   both NULL: pos = s (HF's default arange positions per row).
+ * inv_freq: fp32 [D/2] (the model's rotary inv_freq buffer). dt: F32, F16 or BF16 for all of
+ * q, q_delta, k, q_out, k_out. D/2 must be 32, 64 or 128 (D = 64, 128, 256).
+ */
+int esep_rope(const void* q, const int64_t q_strides[3],
+              const void* q_delta, const int64_t qd_strides[3],
+              const void* k, const int64_t k_strides[3],
+              void* q_out, const int64_t qo_strides[3],
+              void* k_out, const int64_t ko_strides[3],
+              int dt, int64_t B, int64_t S, int HQ, int HK, int D,
+              const void* positions, int pos_dt, const int64_t pos_strides[2],
+              const int32_t* cu_seqlens, int n_seq,
+              const float* inv_freq, float sin_sign, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ESEP_BODY_H */
