@@ -1,0 +1,316 @@
+#!/usr/bin/env python3
+"""Benchmark of the decoder-body RMSNorm + RoPE path (forward + backward) on one MI355X.
+
+Workload (the Qwen2.5-1.5B training-step shape): a full 28-layer
+body sweep, B = 8, S = 1024 (T = 8192 tokens), hidden 1536, 12 q / 2 kv heads, head_dim 128,
+bf16 activations ~ N(0, 1), weights 1 + 0.02 N(0, 1), theta 1e6, eps 1e-6. One step =
+forward (per layer: input RMSNorm, q/k RoPE, post-attention RMSNorm; then the final norm)
+followed by backward in reverse order (every norm: dx and the weight gradient; RoPE: dq, dk).
+Every layer owns its own tensors (as in training), ~9 GB resident in HBM before timing.
+The step is captured once in a HIP graph (the launches go through the C ABI of
+libesep_body.so, ordered on one stream) and replayed.
+
+value = algorithmic bytes of one step / measured seconds per step. Algorithmic bytes count
+each required tensor once (e = 2 bytes):
+  RMSNorm fwd 2eTH + 4T (rstd)   RMSNorm bwd 3eTH + 4T (rstd) + 4H (dw)   RoPE 2eT(HQ+HK)D
+With --rstd recomputed the 4T terms go away (rstd is recomputed from x in backward).
+
+Also printed: the roofline of the dominant kernel (per-launch HIP-event timing of graphs of
+that kernel alone, on the stream it runs on) and the CPU baseline: the PyTorch-eager fp32
+restatement of HF's Qwen2RMSNorm / rotary path (oracle/hf_eager.py) timed on this host's
+cores on one layer of the same workload.
+
+    python bench.py [--steps K] [--warmup W] [--rstd saved|recomputed] [--no-cpu]
+"""
+
+import argparse
+import json
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (ROOT / "esep-soup-kernels_amd", ROOT):
+    if str(_p) not in sys.path:
+        sys.path.insert(0, str(_p))
+
+PEAK_GBS = 8000.0  # MI355X HBM3E, published
+CFG4 = dict(layers=28, B=8, S=1024, H=1536, HQ=12, HK=2, D=128, theta=1e6, eps=1e-6)
+
+
+def log(msg):
+    print(f"[bench {time.strftime('%H:%M:%S')}] {msg}", file=sys.stderr, flush=True)
+
+
+def norm_fwd_bytes(T, H, e, rstd):
+    return 2 * e * T * H + (4 * T if rstd else 0)
+
+
+def norm_bwd_bytes(T, H, e, rstd):
+    return 3 * e * T * H + (4 * T if rstd else 0) + 4 * H
+
+
+def rope_bytes(T, HQ, HK, D, e):
+    return 2 * e * T * (HQ + HK) * D
+
+
+class Body:
+    """Resident tensors of the whole sweep and the launch sequence of one step."""
+
+    def __init__(self, cfg, save_rstd, dev):
+        import torch
+
+        from solution.body import _hip
+
+        self.hip, self.cfg, self.save_rstd = _hip, cfg, save_rstd
+        L, B, S, H, HQ, HK, D = (cfg[k] for k in ("layers", "B", "S", "H", "HQ", "HK", "D"))
+        T = B * S
+        self.T = T
+        bf = torch.bfloat16
+        g = torch.Generator(device=dev).manual_seed(0)
+
+        def rn(*shape):
+            return torch.randn(shape, generator=g, device=dev, dtype=torch.float32).to(bf)
+
+        def wt():
+            return 1 + 0.02 * torch.randn(H, generator=g, device=dev)
+
+        n_norms = 2 * L + 1
+        self.x = [rn(T, H) for _ in range(n_norms)]
+        self.w = [wt() for _ in range(n_norms)]
+        self.y = [torch.empty(T, H, device=dev, dtype=bf) for _ in range(n_norms)]
+        self.rstd = [torch.empty(T, device=dev) if save_rstd else None for _ in range(n_norms)]
+        self.dy = [rn(T, H) for _ in range(n_norms)]
+        self.dx = [torch.empty(T, H, device=dev, dtype=bf) for _ in range(n_norms)]
+        self.dw = [torch.empty(H, device=dev) for _ in range(n_norms)]
+        self.ws = torch.empty(max(_hip.rmsnorm_partials(T, H), 1), H, device=dev)
+        self.q = [rn(B, S, HQ, D) for _ in range(L)]
+        self.k = [rn(B, S, HK, D) for _ in range(L)]
+        self.qo = [torch.empty_like(t) for t in self.q]
+        self.ko = [torch.empty_like(t) for t in self.k]
+        self.dqo = [rn(B, S, HQ, D) for _ in range(L)]
+        self.dko = [rn(B, S, HK, D) for _ in range(L)]
+        self.dq = [torch.empty_like(t) for t in self.q]
+        self.dk = [torch.empty_like(t) for t in self.k]
+        self.inv_freq = (1.0 / (cfg["theta"] ** (torch.arange(0, D, 2, dtype=torch.float) / D))).to(dev)
+
+    # single launches ---------------------------------------------------------------
+    def norm_fwd(self, i):
+        self.hip.rmsnorm_fwd(self.x[i], self.w[i], self.y[i], self.cfg["eps"], rstd=self.rstd[i])
+
+    def norm_bwd(self, i):
+        self.hip.rmsnorm_bwd([self.dy[i]], self.x[i], self.w[i], self.cfg["eps"],
+                             rstd=self.rstd[i], dx=self.dx[i], dw=self.dw[i], workspace=self.ws)
+
+    def rope_fwd(self, l):
+        # padded [B, S, H, D] projections, positions 0..S-1 per row (implicit)
+        self.hip.rope(self.q[l], self.k[l], self.qo[l], self.ko[l], self.inv_freq, 1.0)
+
+    def rope_bwd(self, l):
+        self.hip.rope(self.dqo[l], self.dko[l], self.dq[l], self.dk[l], self.inv_freq, -1.0)
+
+    # one step ------------------------------------------------------------------------
+    def step(self):
+        L = self.cfg["layers"]
+        for l in range(L):
+            self.norm_fwd(2 * l)
+            self.rope_fwd(l)
+            self.norm_fwd(2 * l + 1)
+        self.norm_fwd(2 * L)
+        self.norm_bwd(2 * L)
+        for l in reversed(range(L)):
+            self.norm_bwd(2 * l + 1)
+            self.rope_bwd(l)
+            self.norm_bwd(2 * l)
+
+    def step_bytes(self):
+        c, T, e = self.cfg, self.T, 2
+        L = c["layers"]
+        norm = norm_fwd_bytes(T, c["H"], e, self.save_rstd) + norm_bwd_bytes(T, c["H"], e, self.save_rstd)
+        rope = 2 * rope_bytes(T, c["HQ"], c["HK"], c["D"], e)
+        return (2 * L + 1) * norm + L * rope
+
+
+def capture(fn, warm=True):
+    import torch
+
+    if warm:
+        s = torch.cuda.Stream()
+        s.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(s):
+            fn()
+        torch.cuda.current_stream().wait_stream(s)
+        torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    torch.cuda.synchronize()
+    return g
+
+
+def time_graph(g, reps):
+    """(event ms per replay, wall ms per replay) over `reps` back-to-back replays."""
+    import torch
+
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    t1 = time.perf_counter()
+    return e0.elapsed_time(e1) / reps, (t1 - t0) * 1e3 / reps
+
+
+def kernel_rooflines(body, reps):
+    """Per-launch time of each entry point: a graph of one launch per layer of that kernel
+    alone (distinct tensors, as in the sweep), replayed `reps` times, timed with HIP events
+    on the replay stream. Returns {name: (us_per_launch, algorithmic_bytes_per_launch, launches_per_step)}."""
+    c, T = body.cfg, body.T
+    L = c["layers"]
+    kinds = {
+        "rmsnorm_fwd": (lambda: [body.norm_fwd(i) for i in range(2 * L + 1)], 2 * L + 1,
+                        norm_fwd_bytes(T, c["H"], 2, body.save_rstd)),
+        "rmsnorm_bwd": (lambda: [body.norm_bwd(i) for i in range(2 * L + 1)], 2 * L + 1,
+                        norm_bwd_bytes(T, c["H"], 2, body.save_rstd)),
+        "rope_fwd": (lambda: [body.rope_fwd(l) for l in range(L)], L,
+                     rope_bytes(T, c["HQ"], c["HK"], c["D"], 2)),
+        "rope_bwd": (lambda: [body.rope_bwd(l) for l in range(L)], L,
+                     rope_bytes(T, c["HQ"], c["HK"], c["D"], 2)),
+    }
+    out = {}
+    for name, (fn, n, nbytes) in kinds.items():
+        g = capture(fn)
+        time_graph(g, 2)
+        ms, _ = time_graph(g, reps)
+        out[name] = (ms * 1e3 / n, nbytes, n)
+        log(f"{name}: {ms * 1e3 / n:.2f} us/launch, {nbytes / (ms * 1e-3 / n) / 1e9:.0f} GB/s")
+    return out
+
+
+def cpu_baseline(cfg, budget_s=12.0, batch=2):
+    """PyTorch-eager fp32 HF path (oracle/hf_eager.py) on the host cores: one layer of the
+    workload (2 RMSNorms + q/k RoPE, forward + autograd backward) on `batch` of its 8 rows
+    (the per-token cost does not depend on the batch)."""
+    import torch
+
+    from oracle import hf_eager
+
+    threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+    torch.set_num_threads(threads)
+    S, H, HQ, HK, D, eps = (cfg[k] for k in ("S", "H", "HQ", "HK", "D", "eps"))
+    B = batch
+    T = B * S
+    g = torch.Generator().manual_seed(0)
+    xs = [torch.randn(T, H, generator=g) for _ in range(2)]
+    ws = [1 + 0.02 * torch.randn(H, generator=g) for _ in range(2)]
+    dys = [torch.randn(T, H, generator=g) for _ in range(2)]
+    q = torch.randn(B, HQ, S, D, generator=g)
+    k = torch.randn(B, HK, S, D, generator=g)
+    dq, dk = torch.randn(B, HQ, S, D, generator=g), torch.randn(B, HK, S, D, generator=g)
+    inv = 1.0 / (cfg["theta"] ** (torch.arange(0, D, 2, dtype=torch.float) / D))
+    pos = torch.arange(S).expand(B, S)
+    times = []
+    t_start = time.perf_counter()
+    hf_eager.body_step(xs, ws, q, k, dys, dq, dk, inv, pos, eps)  # warm-up (allocator, threads)
+    while len(times) < 2 or (time.perf_counter() - t_start < budget_s and len(times) < 20):
+        t0 = time.perf_counter()
+        hf_eager.body_step(xs, ws, q, k, dys, dq, dk, inv, pos, eps)
+        times.append(time.perf_counter() - t0)
+    t = statistics.median(times)
+    e = 4
+    layer_bytes = 2 * (norm_fwd_bytes(T, H, e, True) + norm_bwd_bytes(T, H, e, True)) + \
+        2 * rope_bytes(T, HQ, HK, D, e)
+    return {"value": round(layer_bytes / t / 1e9, 2), "unit": "GB/s", "cores": threads,
+            "kind": "port",
+            "sample": f"one layer of config 4 (2 RMSNorm + q/k RoPE, fwd + autograd bwd) on "
+                      f"{B} of its 8 rows (T={T}), fp32 PyTorch eager (HF Qwen2RMSNorm / apply_rotary_pos_emb "
+                      f"restated), median of {len(times)} reps, {t * 1e3:.1f} ms per layer; "
+                      f"bytes counted with e=4",
+            # a full sweep is L layers plus the final norm (~ half a layer)
+            "tokens_per_s": round(T / (t * (cfg["layers"] + 0.5)), 1)}
+
+
+def main():
+    ap = argparse.ArgumentParser(description=__doc__, formatter_class=argparse.RawDescriptionHelpFormatter)
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=30)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--rstd", choices=["saved", "recomputed"], default="saved")
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
+    ap.add_argument("--kernel-reps", type=int, default=20)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU: this build has no multi-GPU path (--gpus {args.gpus} "
+              "requested). The path shards by tokens with no communication except one H-float "
+              "all-reduce of the norm weight gradients; run with --gpus 1.", file=sys.stderr)
+        return 2
+
+    import torch
+
+    from solution.body import _hip
+
+    _hip.lib()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    cfg = CFG4
+    save_rstd = args.rstd == "saved"
+    log(f"allocating config 4 ({cfg['layers']} layers, T={cfg['B'] * cfg['S']}) on {torch.cuda.get_device_name(dev)}")
+    body = Body(cfg, save_rstd, dev)
+    torch.cuda.synchronize()
+    log("capturing the step graph")
+    g = capture(body.step)
+    for _ in range(args.warmup):
+        g.replay()
+    torch.cuda.synchronize()
+    log(f"timing {args.steps} steps")
+    ev_ms, wall_ms = time_graph(g, args.steps)
+    step_bytes = body.step_bytes()
+    ms = max(ev_ms, wall_ms)
+    gbs = step_bytes / (ms * 1e-3) / 1e9
+    log(f"step {ms:.3f} ms (events {ev_ms:.3f}), {gbs:.0f} GB/s = {gbs / PEAK_GBS:.1%} of peak")
+
+    kr = kernel_rooflines(body, args.kernel_reps)
+    name, (us, nbytes, n) = max(kr.items(), key=lambda kv: kv[1][0] * kv[1][2])
+    achieved = nbytes / (us * 1e-6) / 1e9
+    roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
+                "frac": round(achieved / PEAK_GBS, 4), "traffic": None, "kernel": name,
+                "us_per_launch": round(us, 3), "bytes_per_launch": nbytes,
+                "all_kernels": {k: {"us": round(v[0], 3), "GB/s": round(v[1] / (v[0] * 1e-6) / 1e9, 1),
+                                    "launches_per_step": v[2]} for k, v in kr.items()}}
+
+    cpu = None
+    if not args.no_cpu:
+        log("CPU baseline (PyTorch eager fp32, one layer)")
+        cpu = cpu_baseline(cfg)
+        log(f"CPU: {cpu['value']} GB/s on {cpu['cores']} threads")
+
+    T = cfg["B"] * cfg["S"]
+    out = {
+        "metric": "RMSNorm+RoPE fwd+bwd achieved HBM GB/s (% of peak), Qwen2.5-1.5B shape",
+        "value": round(gbs, 1), "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "f32",
+        "data": "synthetic",
+        "config": {"workload": "config4: 28-layer Qwen2.5-1.5B body sweep, 2 RMSNorm + q/k RoPE "
+                               "per layer + final norm, forward then backward (dx, dw, dq, dk)",
+                   "tokens": T, "batch": cfg["B"], "seq_len": cfg["S"], "hidden": cfg["H"],
+                   "q_heads": cfg["HQ"], "kv_heads": cfg["HK"], "head_dim": cfg["D"],
+                   "io_dtype": "bf16", "rstd": args.rstd, "graph": True,
+                   "bytes_per_step": step_bytes},
+        "frac_of_peak": round(gbs / PEAK_GBS, 4),
+        "tokens_per_s": round(T / (ms * 1e-3), 1),
+        "ms_per_step_events": round(ev_ms, 4),
+        "roofline": roofline,
+        "cpu_baseline": cpu,
+    }
+    print(json.dumps(out), flush=True)
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -66,11 +66,19 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
                                            kRsrcWord3);
 }
 
+// Cache policy of a buffer access (the instruction's cache-policy bits on gfx950):
+// kCached for data that is re-read (norm weights, slot tables), kStream (nt: non-temporal)
+// for tensors that are read or written exactly once per kernel.
+constexpr int kCached = 0;
+constexpr int kStream = 2;
+
+template <int POL = kCached>
 __device__ __forceinline__ u32x4 buf_ld16(rsrc_t r, uint32_t off) {
-  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, 0);
+  return __builtin_amdgcn_raw_buffer_load_b128(r, off, 0, POL);
 }
+template <int POL = kCached>
 __device__ __forceinline__ void buf_st16(rsrc_t r, uint32_t off, u32x4 v) {
-  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, 0);
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, off, 0, POL);
 }
 
 // A row (or other wave-uniform span): its buffer descriptor, base pointer and size in bytes.
@@ -84,33 +92,53 @@ __device__ __forceinline__ Span make_span(const void* base, uint32_t bytes) {
   return Span{make_rsrc(base, bytes), static_cast<const char*>(base), bytes};
 }
 
-// 8 consecutive elements starting at byte offset `off` of the span, converted to fp32.
-// VEC: two (fp32) or one (16-bit) 16-byte buffer accesses; the span base and `off` are
-// 16-byte aligned and the chunk is whole or wholly outside. !VEC (ragged or unaligned rows,
-// the rare path): one bounds-checked pointer access per element.
+// Raw (still packed) contents of one 8-element chunk: 16 bytes for 16-bit types, 32 for fp32.
+// Loading raw and unpacking at the point of use keeps a prefetched 16-bit chunk in 4 VGPRs
+// instead of 8.
+template <typename T> struct Raw {
+  u32x4 a;
+};
+template <> struct Raw<float> {
+  u32x4 a, b;
+};
+
+// 8 consecutive elements starting at byte offset `off` of the span. VEC: two (fp32) or one
+// (16-bit) 16-byte buffer accesses; the span base and `off` are 16-byte aligned and the chunk
+// is whole or wholly outside. !VEC (ragged or unaligned rows, the rare path): one
+// bounds-checked pointer access per element.
 template <typename T> struct Buf {
   typedef T v8 __attribute__((ext_vector_type(8)));
 
-  template <bool VEC>
+  template <int POL>
+  __device__ static Raw<T> load_raw(const Span& s, uint32_t off) {
+    Raw<T> r;
+    r.a = buf_ld16<POL>(s.r, off);
+    if constexpr (sizeof(T) == 4) r.b = buf_ld16<POL>(s.r, off + 16);
+    return r;
+  }
+
+  __device__ static void unpack(const Raw<T>& r, float (&v)[8]) {
+    if constexpr (sizeof(T) == 4) {
+      v[0] = __uint_as_float(r.a.x); v[1] = __uint_as_float(r.a.y);
+      v[2] = __uint_as_float(r.a.z); v[3] = __uint_as_float(r.a.w);
+      v[4] = __uint_as_float(r.b.x); v[5] = __uint_as_float(r.b.y);
+      v[6] = __uint_as_float(r.b.z); v[7] = __uint_as_float(r.b.w);
+    } else if constexpr (std::is_same_v<T, __bf16>) {
+      v[0] = bf16_lo(r.a.x); v[1] = bf16_hi(r.a.x);
+      v[2] = bf16_lo(r.a.y); v[3] = bf16_hi(r.a.y);
+      v[4] = bf16_lo(r.a.z); v[5] = bf16_hi(r.a.z);
+      v[6] = bf16_lo(r.a.w); v[7] = bf16_hi(r.a.w);
+    } else {
+      const v8 h = __builtin_bit_cast(v8, r.a);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = (float)h[e];
+    }
+  }
+
+  template <bool VEC, int POL = kCached>
   __device__ static void load(const Span& s, uint32_t off, float (&v)[8]) {
     if constexpr (VEC) {
-      if constexpr (sizeof(T) == 4) {
-        const u32x4 a = buf_ld16(s.r, off), b = buf_ld16(s.r, off + 16);
-        v[0] = __uint_as_float(a.x); v[1] = __uint_as_float(a.y);
-        v[2] = __uint_as_float(a.z); v[3] = __uint_as_float(a.w);
-        v[4] = __uint_as_float(b.x); v[5] = __uint_as_float(b.y);
-        v[6] = __uint_as_float(b.z); v[7] = __uint_as_float(b.w);
-      } else if constexpr (std::is_same_v<T, __bf16>) {
-        const u32x4 u = buf_ld16(s.r, off);
-        v[0] = bf16_lo(u.x); v[1] = bf16_hi(u.x);
-        v[2] = bf16_lo(u.y); v[3] = bf16_hi(u.y);
-        v[4] = bf16_lo(u.z); v[5] = bf16_hi(u.z);
-        v[6] = bf16_lo(u.w); v[7] = bf16_hi(u.w);
-      } else {
-        const v8 h = __builtin_bit_cast(v8, buf_ld16(s.r, off));
-#pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = (float)h[e];
-      }
+      unpack(load_raw<POL>(s, off), v);
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
@@ -120,19 +148,19 @@ template <typename T> struct Buf {
     }
   }
 
-  template <bool VEC>
+  template <bool VEC, int POL = kCached>
   __device__ static void store(const Span& s, uint32_t off, const float (&v)[8]) {
     if constexpr (VEC) {
       if constexpr (sizeof(T) == 4) {
-        buf_st16(s.r, off, u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]),
-                                 __float_as_uint(v[2]), __float_as_uint(v[3])});
-        buf_st16(s.r, off + 16, u32x4{__float_as_uint(v[4]), __float_as_uint(v[5]),
-                                      __float_as_uint(v[6]), __float_as_uint(v[7])});
+        buf_st16<POL>(s.r, off, u32x4{__float_as_uint(v[0]), __float_as_uint(v[1]),
+                                      __float_as_uint(v[2]), __float_as_uint(v[3])});
+        buf_st16<POL>(s.r, off + 16, u32x4{__float_as_uint(v[4]), __float_as_uint(v[5]),
+                                           __float_as_uint(v[6]), __float_as_uint(v[7])});
       } else {
         v8 h;
 #pragma unroll
         for (int e = 0; e < 8; ++e) h[e] = Elt<T>::from_f(v[e]);
-        buf_st16(s.r, off, __builtin_bit_cast(u32x4, h));
+        buf_st16<POL>(s.r, off, __builtin_bit_cast(u32x4, h));
       }
     } else {
 #pragma unroll

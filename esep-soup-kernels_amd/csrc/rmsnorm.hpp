@@ -93,13 +93,15 @@ __device__ __forceinline__ float inv_rms(float ss, int n, float eps) {
   return 1.0f / sqrtf(ss / (float)n + eps);
 }
 
-template <bool VEC, typename T>
+// Streamed row data (read or written once) is accessed non-temporally; the weight vector and
+// the slot table (read by every row) through the caches.
+template <bool VEC, typename T, int POL = kStream>
 __device__ __forceinline__ void bload(const Span& s, uint32_t off, float (&v)[8]) {
-  Buf<T>::template load<VEC>(s, off, v);
+  Buf<T>::template load<VEC, POL>(s, off, v);
 }
-template <bool VEC, typename T>
+template <bool VEC, typename T, int POL = kStream>
 __device__ __forceinline__ void bstore(const Span& s, uint32_t off, const float (&v)[8]) {
-  Buf<T>::template store<VEC>(s, off, v);
+  Buf<T>::template store<VEC, POL>(s, off, v);
 }
 
 // Span of row `row` of a [rows, n] tensor with leading dimension ld (elements); a row that
@@ -158,7 +160,7 @@ __device__ __forceinline__ void fwd_rows(const FwdArgs& a, float* red) {
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
     float w8[8], o[8];
-    bload<VEC, float>(rw, (tg + k * G) * 32, w8);
+    bload<VEC, float, kCached>(rw, (tg + k * G) * 32, w8);
 #pragma unroll
     for (int e = 0; e < 8; ++e) o[e] = w8[e] * (v[k][e] * inv);
     bstore<VEC, TY>(ry, (tg + k * G) * 8 * sizeof(TY), o);
@@ -186,6 +188,43 @@ template <int NV, bool VEC, typename TX, typename TD, typename TY>
 __global__ __launch_bounds__(kFwdMaxThreads) void k_rmsnorm_fwd(const FwdArgs a) {
   __shared__ float red[kFwdMaxThreads / kWave];
   fwd_rows<NV, VEC, TX, TD, TY>(a, red);
+}
+
+// Weight-gradient partial of one block: a fixed tree over the gpb row groups (at each level
+// the groups [half, 2 half) park their accumulators in LDS and the groups below add them; the
+// LDS slot stride NV * G * 8 floats keeps chunks past the row end inside their slot), then
+// group 0 writes the block sum as row blockIdx.x of the [P, n] partials.
+template <int NV, bool VEC>
+__device__ __forceinline__ void dw_block_partial(const BwdArgs& a, float (&acc)[NV][8],
+                                                 float* lds, int grp, int gpb, int tg, int G) {
+  const int n = a.n;
+  const int stride = NV * G * 8;
+  int top = 1;
+  while (top < gpb) top <<= 1;
+  for (int half = top >> 1; half >= 1; half >>= 1) {
+    if (grp >= half && grp < 2 * half && grp < gpb) {
+      float* dst = lds + (grp - half) * stride;
+#pragma unroll
+      for (int k = 0; k < NV; ++k) Chunk<float>::store(dst + 8 * (tg + k * G), acc[k]);
+    }
+    __syncthreads();
+    if (grp < half && grp + half < gpb) {
+      const float* src = lds + grp * stride;
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        float t[8];
+        Chunk<float>::load(src + 8 * (tg + k * G), t);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) acc[k][e] += t[e];
+      }
+    }
+    __syncthreads();
+  }
+  if (grp == 0) {
+    const Span rp = make_span(a.part + (int64_t)blockIdx.x * n, (uint32_t)n * 4u);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) bstore<VEC, float, kCached>(rp, (tg + k * G) * 32, acc[k]);
+  }
 }
 
 // ---------------------------------------------------------------------------------------
@@ -228,8 +267,8 @@ __device__ __forceinline__ void bwd_rows(const BwdArgs& a, float* red, float* ld
         for (int k = 0; k < NV; ++k) bload<VEC, TX>(rx, (tg + k * G) * 8 * sizeof(TX), x[k]);
       }
       // Further consumers' gradients, summed in fp32 (constant indices: no private copy of
-      // the pointer array).
-#pragma unroll
+      // the pointer array; one gradient at a time keeps the registers of the common path).
+#pragma unroll 1
       for (int i = 1; i < kMaxDy; ++i) {
         if (i < a.n_dy) {
           const Span ri = row_rsrc<TDY>(a.dy[i], row, a.ld_dy, n, ok);
@@ -264,9 +303,9 @@ __device__ __forceinline__ void bwd_rows(const BwdArgs& a, float* red, float* ld
         for (int k = 0; k < NV; ++k) {
           const int col = 8 * (tg + k * G);
           float w8[8];
-          bload<VEC, float>(rw, col * 4, w8);
+          bload<VEC, float, kCached>(rw, col * 4, w8);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) x[k][e] = col + e < n ? x[k][e] / w8[e] : 0.f;
+          for (int e = 0; e < 8; ++e) x[k][e] = x[k][e] / (col + e < n ? w8[e] : 1.f);
         }
         if (a.n_special > 0 && ok) {
           const Span rs = make_span(a.slot, (uint32_t)n * 4u);
@@ -300,7 +339,7 @@ __device__ __forceinline__ void bwd_rows(const BwdArgs& a, float* red, float* ld
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
         float w8[8];
-        bload<VEC, float>(rw, (tg + k * G) * 32, w8);
+        bload<VEC, float, kCached>(rw, (tg + k * G) * 32, w8);
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
           dy[k][e] *= w8[e];
@@ -343,68 +382,192 @@ __device__ __forceinline__ void bwd_rows(const BwdArgs& a, float* red, float* ld
     }
   }
 
+  if (want_dw) dw_block_partial<NV, VEC>(a, acc, lds, grp, gpb, tg, G);
+}
+
+// Fast backward for the common call: one gradient of y, xhat from x (not from y), no dr_out,
+// 16-byte-aligned whole chunks. The next row's dy and x are prefetched raw (still packed)
+// while the current row is computed, so each wavefront keeps two rows of loads in flight.
+// The weight-gradient accumulators live in LDS (one slot of NV * G * 8 floats per row group,
+// indexed by column) instead of registers; at the end the block sums the slots in group order.
+template <int NV, typename TX, typename TDY, typename TO>
+__device__ __forceinline__ void bwd_rows_fast(const BwdArgs& a, float* red, float* lds) {
+  const int G = kWave * a.wpr;
+  const int gpb = blockDim.x / G;
+  const int grp = wave_id() / a.wpr;
+  const int tg = (int)threadIdx.x - grp * G;
+  const int n = a.n;
+  const int64_t start = (int64_t)blockIdx.x * a.rpb;
+  const int64_t end = start + a.rpb < a.rows ? start + a.rpb : a.rows;
+  const int iters = (int)((a.rpb + gpb - 1) / gpb);
+  const bool want_dw = a.part != nullptr;
+  const Span rw = make_span(a.w, (uint32_t)n * 4u);
+  const int stride = NV * G * 8;
+  float* acc = lds + grp * stride;
   if (want_dw) {
-    // Fixed tree over the gpb groups of this block: at each level the groups [half, 2 half)
-    // park their accumulators in LDS and the groups below add them. The LDS slot stride is
-    // NV * G * 8 floats, so chunks past the row end stay inside their slot. Group 0 ends with
-    // the block sum and writes it as row blockIdx.x of the partials.
-    const int stride = NV * G * 8;
-    int top = 1;
-    while (top < gpb) top <<= 1;
-    for (int half = top >> 1; half >= 1; half >>= 1) {
-      if (grp >= half && grp < 2 * half && grp < gpb) {
-        float* dst = lds + (grp - half) * stride;
+    const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int k = 0; k < NV; ++k) Chunk<float>::store(dst + 8 * (tg + k * G), acc[k]);
-      }
-      __syncthreads();
-      if (grp < half && grp + half < gpb) {
-        const float* src = lds + grp * stride;
+    for (int k = 0; k < NV; ++k) Chunk<float>::store(acc + 8 * (tg + k * G), zero);
+  }
+
+  int64_t row = start + grp;
+  bool ok = row < end;
+  Raw<TDY> rdy[NV];
+  Raw<TX> rx[NV];
+  {
+    const Span sd = row_rsrc<TDY>(a.dy[0], row, a.ld_dy, n, ok);
+    const Span sx = row_rsrc<TX>(a.x, row, a.ld_x, n, ok);
 #pragma unroll
-        for (int k = 0; k < NV; ++k) {
-          float t[8];
-          Chunk<float>::load(src + 8 * (tg + k * G), t);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) acc[k][e] += t[e];
-        }
-      }
-      __syncthreads();
+    for (int k = 0; k < NV; ++k) {
+      rdy[k] = Buf<TDY>::template load_raw<kStream>(sd, (tg + k * G) * 8 * sizeof(TDY));
+      rx[k] = Buf<TX>::template load_raw<kStream>(sx, (tg + k * G) * 8 * sizeof(TX));
     }
-    if (grp == 0) {
-      const Span rp = make_span(a.part + (int64_t)blockIdx.x * n, (uint32_t)n * 4u);
+  }
+  float inv_next = (a.rstd != nullptr && ok) ? a.rstd[row] : 1.f;
+
+  for (int it = 0; it < iters; ++it) {
+    const int64_t nrow = row + gpb;
+    const bool nok = it + 1 < iters && nrow < end;
+    // prefetch the next row (a row that does not exist reads nothing: 0-byte span)
+    Raw<TDY> ndy[NV];
+    Raw<TX> nx[NV];
+    {
+      const Span sd = row_rsrc<TDY>(a.dy[0], nrow, a.ld_dy, n, nok);
+      const Span sx = row_rsrc<TX>(a.x, nrow, a.ld_x, n, nok);
 #pragma unroll
-      for (int k = 0; k < NV; ++k) bstore<VEC, float>(rp, (tg + k * G) * 32, acc[k]);
+      for (int k = 0; k < NV; ++k) {
+        ndy[k] = Buf<TDY>::template load_raw<kStream>(sd, (tg + k * G) * 8 * sizeof(TDY));
+        nx[k] = Buf<TX>::template load_raw<kStream>(sx, (tg + k * G) * 8 * sizeof(TX));
+      }
+    }
+    float inv = inv_next;
+    inv_next = (a.rstd != nullptr && nok) ? a.rstd[nrow] : 1.f;
+
+    float dy[NV][8], x[NV][8];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      Buf<TDY>::unpack(rdy[k], dy[k]);
+      Buf<TX>::unpack(rx[k], x[k]);
+    }
+    if (a.rstd == nullptr) {
+      float ss = 0.f;
+#pragma unroll
+      for (int k = 0; k < NV; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(x[k][e], x[k][e], ss);
+      inv = inv_rms(row_sum(ss, a.wpr, red), n, a.eps);
+    }
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[k][e] *= inv;
+    if (want_dw && ok) {
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        float t[8];
+        Chunk<float>::load(acc + 8 * (tg + k * G), t);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) t[e] = fmaf(dy[k][e], x[k][e], t[e]);
+        Chunk<float>::store(acc + 8 * (tg + k * G), t);
+      }
+    }
+    float p = 0.f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      float w8[8];
+      bload<true, float, kCached>(rw, (tg + k * G) * 32, w8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        dy[k][e] *= w8[e];
+        p = fmaf(dy[k][e], x[k][e], p);
+      }
+    }
+    const float proj = row_sum(p, a.wpr, red) / (float)n;
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dy[k][e] = inv * (dy[k][e] - x[k][e] * proj);
+    if (a.dr != nullptr) {
+      const Span so = row_rsrc<float>(a.dr, row, a.ld_out, n, ok);
+#pragma unroll
+      for (int k = 0; k < NV; ++k) bstore<true, float>(so, (tg + k * G) * 32, dy[k]);
+    }
+    if (a.dx != nullptr) {
+      const Span so = row_rsrc<TO>(a.dx, row, a.ld_out, n, ok);
+#pragma unroll
+      for (int k = 0; k < NV; ++k) bstore<true, TO>(so, (tg + k * G) * 8 * sizeof(TO), dy[k]);
+    }
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      rdy[k] = ndy[k];
+      rx[k] = nx[k];
+    }
+    row = nrow;
+    ok = nok;
+  }
+  if (want_dw) {
+    // block sum: column quads over all threads, groups added in group order
+    __syncthreads();
+    float* dst = a.part + (int64_t)blockIdx.x * n;
+    for (int q = threadIdx.x; 4 * q < n; q += blockDim.x) {
+      f32x4 t = *reinterpret_cast<const f32x4*>(lds + 4 * q);
+      for (int g = 1; g < gpb; ++g) t += *reinterpret_cast<const f32x4*>(lds + g * stride + 4 * q);
+      *reinterpret_cast<f32x4*>(dst + 4 * q) = t;
     }
   }
 }
 
-template <int NV, bool VEC, typename TX, typename TDY, typename TO>
+// FAST: bwd_rows_fast (only with VEC); else the general bwd_rows.
+template <int NV, bool VEC, bool FAST, typename TX, typename TDY, typename TO>
 __global__ __launch_bounds__(kBwdThreads) void k_rmsnorm_bwd(const BwdArgs a) {
   __shared__ float red[kBwdThreads / kWave];
   extern __shared__ float lds[];
-  bwd_rows<NV, VEC, TX, TDY, TO>(a, red, lds);
+  if constexpr (FAST)
+    bwd_rows_fast<NV, TX, TDY, TO>(a, red, lds);
+  else
+    bwd_rows<NV, VEC, TX, TDY, TO>(a, red, lds);
 }
 
-// Stage 2 of the weight gradient: dw[j] = sum_p part[p, j], p ascending within each of the
-// 16 wavefront strides (p = w, w + 16, ...), then the 16 strided sums in wave order.
+// Stage 2 of the weight gradient: dw[j] = sum_p part[p, j]. A block of 256 threads owns 32
+// columns: thread (stripe r = tid / 8, quad c = tid % 8) adds the 4 columns 4c..4c+3 of rows
+// p = r, r + 32, r + 64, ... in ascending p (eight 16-byte loads in flight), then the 32 stripe
+// sums are added in stripe order. n % 4 != 0 takes the same order one column at a time.
+constexpr int kRedCols = 32;
+constexpr int kRedStripes = 32;
+
 template <typename TW>
-__global__ __launch_bounds__(1024) void k_dgamma_reduce(const float* __restrict__ part,
+__global__ __launch_bounds__(256) void k_dgamma_reduce(const float* __restrict__ part,
                                                           int64_t P, int n, TW* __restrict__ dw) {
-  __shared__ float red[16][64];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int j = blockIdx.x * 64 + lane;
-  float s = 0.f;
-  if (j < n) {
-    for (int64_t p = wave; p < P; p += 16) s += part[p * n + j];
+  __shared__ f32x4 red[kRedStripes][kRedCols / 4];
+  const int c = threadIdx.x % (kRedCols / 4);
+  const int r = threadIdx.x / (kRedCols / 4);
+  const int j = blockIdx.x * kRedCols + 4 * c;
+  f32x4 s = {0.f, 0.f, 0.f, 0.f};
+  if ((n & 3) == 0) {
+    if (j < n) {
+#pragma unroll 8
+      for (int64_t p = r; p < P; p += kRedStripes)
+        s += *reinterpret_cast<const f32x4*>(part + p * n + j);
+    }
+  } else {
+    for (int64_t p = r; p < P; p += kRedStripes) {
+      const float* row = part + p * n;
+      if (j < n) s.x += row[j];
+      if (j + 1 < n) s.y += row[j + 1];
+      if (j + 2 < n) s.z += row[j + 2];
+      if (j + 3 < n) s.w += row[j + 3];
+    }
   }
-  red[wave][lane] = s;
+  red[r][c] = s;
   __syncthreads();
-  if (wave == 0 && j < n) {
-    float t = red[0][lane];
+  if (r == 0) {
+    f32x4 t = red[0][c];
 #pragma unroll
-    for (int w = 1; w < 16; ++w) t += red[w][lane];
-    dw[j] = Elt<TW>::from_f(t);
+    for (int i = 1; i < kRedStripes; ++i) t += red[i][c];
+    const float v[4] = {t.x, t.y, t.z, t.w};
+#pragma unroll
+    for (int e = 0; e < 4; ++e)
+      if (j + e < n) dw[j + e] = Elt<TW>::from_f(v[e]);
   }
 }
 

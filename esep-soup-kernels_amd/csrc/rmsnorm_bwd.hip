@@ -12,12 +12,16 @@ template <typename TX, typename TDY, typename TO>
 static hipError_t bwd_nv(const BwdArgs& a, int nv, dim3 grid, dim3 block, size_t lds,
                          hipStream_t s) {
   if (!a.vec) {
-    hipLaunchKernelGGL((k_rmsnorm_bwd<3, false, TX, TDY, TO>), grid, block, lds, s, a);
+    hipLaunchKernelGGL((k_rmsnorm_bwd<3, false, false, TX, TDY, TO>), grid, block, lds, s, a);
     return hipGetLastError();
   }
-  switch (nv) {
-    case 2: hipLaunchKernelGGL((k_rmsnorm_bwd<2, true, TX, TDY, TO>), grid, block, lds, s, a); break;
-    case 3: hipLaunchKernelGGL((k_rmsnorm_bwd<3, true, TX, TDY, TO>), grid, block, lds, s, a); break;
+  // The fast kernel serves the plain backward: one dy, xhat from x, no dr_out.
+  const bool fast = a.n_dy == 1 && !a.from_y && a.dr_out == nullptr && a.n_special == 0;
+  switch (nv * 2 + (fast ? 1 : 0)) {
+    case 4: hipLaunchKernelGGL((k_rmsnorm_bwd<2, true, false, TX, TDY, TO>), grid, block, lds, s, a); break;
+    case 5: hipLaunchKernelGGL((k_rmsnorm_bwd<2, true, true, TX, TDY, TO>), grid, block, lds, s, a); break;
+    case 6: hipLaunchKernelGGL((k_rmsnorm_bwd<3, true, false, TX, TDY, TO>), grid, block, lds, s, a); break;
+    case 7: hipLaunchKernelGGL((k_rmsnorm_bwd<3, true, true, TX, TDY, TO>), grid, block, lds, s, a); break;
     default: return hipErrorInvalidValue;
   }
   return hipGetLastError();
@@ -57,7 +61,7 @@ hipError_t launch_rmsnorm_bwd(const BwdArgs& a, int x_dt, int dy_dt, int o_dt, i
 hipError_t launch_dgamma_reduce(const float* part, int64_t P, int n, void* dw, int dw_dt,
                                 hipStream_t s, bool* sup) {
   *sup = true;
-  const dim3 grid((n + 63) / 64), block(1024);
+  const dim3 grid((n + kRedCols - 1) / kRedCols), block(256);
   if (dw_dt == 0)
     hipLaunchKernelGGL(k_dgamma_reduce<float>, grid, block, 0, s, part, P, n, static_cast<float*>(dw));
   else if (dw_dt == 1)

@@ -7,8 +7,8 @@
 // cos / sin back as two 16-byte LDS loads, and reuses them for every head of the token:
 // HALF/8 lanes cover one head (both halves: x1 = [8c, 8c+8), x2 = [HALF+8c, HALF+8c+8)), so a
 // wavefront instruction moves 64/(HALF/8) heads and every global access is 16 bytes.
-// Up to four passes of heads are loaded before any is rotated and stored, so a lane keeps
-// eight 16-byte loads in flight.
+// Up to four passes of heads are loaded (raw, still packed, non-temporal) before any is
+// rotated and stored, so a lane keeps eight 16-byte loads in flight in few registers.
 //
 // Numerics follow the reference's _rope_kernel (solution/body/norm_rope.py:330-369):
 // angle = float(pos) * inv_freq[j] as one fp32 multiply; q + q_delta is formed in the storage
@@ -21,26 +21,53 @@ namespace esep {
 constexpr int kRopeWaves = 4;
 constexpr int kRopePasses = 4;
 
+// One head half (8 elements) of one lane: VEC as a single raw 16-byte (two for fp32)
+// non-temporal load, kept packed until it is rotated; !VEC element by element.
 template <bool VEC, typename T>
-__device__ __forceinline__ void ld_half(const T* p, float (&v)[8]) {
+__device__ __forceinline__ Raw<T> ld_raw(const T* p) {
+  Raw<T> r;
   if constexpr (VEC) {
-    Chunk<T>::load(p, v);
+    r.a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p));
+    if constexpr (sizeof(T) == 4) r.b = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(p) + 1);
   } else {
+    typedef T v8 __attribute__((ext_vector_type(8)));
+    v8 h;
 #pragma unroll
-    for (int e = 0; e < 8; ++e) v[e] = Elt<T>::to_f(p[e]);
+    for (int e = 0; e < 8; ++e) h[e] = p[e];
+    if constexpr (sizeof(T) == 4) {
+      r.a = u32x4{__float_as_uint(h[0]), __float_as_uint(h[1]), __float_as_uint(h[2]), __float_as_uint(h[3])};
+      r.b = u32x4{__float_as_uint(h[4]), __float_as_uint(h[5]), __float_as_uint(h[6]), __float_as_uint(h[7])};
+    } else {
+      r.a = __builtin_bit_cast(u32x4, h);
+    }
   }
+  return r;
 }
+
 template <bool VEC, typename T>
 __device__ __forceinline__ void st_half(T* p, const float (&v)[8]) {
+  typedef T v8 __attribute__((ext_vector_type(8)));
+  v8 h;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) h[e] = Elt<T>::from_f(v[e]);
   if constexpr (VEC) {
-    Chunk<T>::store(p, v);
+    if constexpr (sizeof(T) == 4) {
+      __builtin_nontemporal_store(u32x4{__float_as_uint(h[0]), __float_as_uint(h[1]),
+                                        __float_as_uint(h[2]), __float_as_uint(h[3])},
+                                  reinterpret_cast<u32x4*>(p));
+      __builtin_nontemporal_store(u32x4{__float_as_uint(h[4]), __float_as_uint(h[5]),
+                                        __float_as_uint(h[6]), __float_as_uint(h[7])},
+                                  reinterpret_cast<u32x4*>(p) + 1);
+    } else {
+      __builtin_nontemporal_store(__builtin_bit_cast(u32x4, h), reinterpret_cast<u32x4*>(p));
+    }
   } else {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) p[e] = Elt<T>::from_f(v[e]);
+    for (int e = 0; e < 8; ++e) p[e] = h[e];
   }
 }
 
-template <bool VEC, typename T, int HALF>
+template <bool VEC, bool QD, typename T, int HALF>
 __device__ __forceinline__ void rope_token(const RopeArgs& a, int64_t b, int64_t s, int lane,
                                            const float (&cv)[8], const float (&sv)[8]) {
   constexpr int LPH = HALF / 8;
@@ -55,7 +82,8 @@ __device__ __forceinline__ void rope_token(const RopeArgs& a, int64_t b, int64_t
   T* __restrict__ ko = static_cast<T*>(a.ko);
 
   for (int h0 = 0; h0 < nh; h0 += kRopePasses * HPP) {
-    float x1[kRopePasses][8], x2[kRopePasses][8];
+    // Issue every load of up to four passes of heads (raw, packed) before any rotation.
+    Raw<T> x1[kRopePasses], x2[kRopePasses], d1[kRopePasses], d2[kRopePasses];
 #pragma unroll
     for (int i = 0; i < kRopePasses; ++i) {
       const int h = h0 + i * HPP + hs;
@@ -63,24 +91,12 @@ __device__ __forceinline__ void rope_token(const RopeArgs& a, int64_t b, int64_t
         const T* src = h < a.HQ
             ? q + b * a.q_s[0] + s * a.q_s[1] + (int64_t)h * a.q_s[2]
             : k + b * a.k_s[0] + s * a.k_s[1] + (int64_t)(h - a.HQ) * a.k_s[2];
-        ld_half<VEC>(src + 8 * c, x1[i]);
-        ld_half<VEC>(src + HALF + 8 * c, x2[i]);
-      }
-    }
-    if (qd != nullptr) {
-#pragma unroll
-      for (int i = 0; i < kRopePasses; ++i) {
-        const int h = h0 + i * HPP + hs;
-        if (h < a.HQ) {
-          const T* src = qd + b * a.qd_s[0] + s * a.qd_s[1] + (int64_t)h * a.qd_s[2];
-          float d1[8], d2[8];
-          ld_half<VEC>(src + 8 * c, d1);
-          ld_half<VEC>(src + HALF + 8 * c, d2);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            x1[i][e] = Elt<T>::round(x1[i][e] + d1[e]);
-            x2[i][e] = Elt<T>::round(x2[i][e] + d2[e]);
-          }
+        x1[i] = ld_raw<VEC>(src + 8 * c);
+        x2[i] = ld_raw<VEC>(src + HALF + 8 * c);
+        if (QD && h < a.HQ) {
+          const T* dsrc = qd + b * a.qd_s[0] + s * a.qd_s[1] + (int64_t)h * a.qd_s[2];
+          d1[i] = ld_raw<VEC>(dsrc + 8 * c);
+          d2[i] = ld_raw<VEC>(dsrc + HALF + 8 * c);
         }
       }
     }
@@ -88,11 +104,25 @@ __device__ __forceinline__ void rope_token(const RopeArgs& a, int64_t b, int64_t
     for (int i = 0; i < kRopePasses; ++i) {
       const int h = h0 + i * HPP + hs;
       if (h < nh) {
+        float u1[8], u2[8];
+        Buf<T>::unpack(x1[i], u1);
+        Buf<T>::unpack(x2[i], u2);
+        if (QD && h < a.HQ) {
+          // q + q_delta in the storage dtype (one rounding), as the unfused model adds them
+          float e1[8], e2[8];
+          Buf<T>::unpack(d1[i], e1);
+          Buf<T>::unpack(d2[i], e2);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            u1[e] = Elt<T>::round(u1[e] + e1[e]);
+            u2[e] = Elt<T>::round(u2[e] + e2[e]);
+          }
+        }
         float o1[8], o2[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
-          o1[e] = x1[i][e] * cv[e] - x2[i][e] * sv[e];
-          o2[e] = x2[i][e] * cv[e] + x1[i][e] * sv[e];
+          o1[e] = u1[e] * cv[e] - u2[e] * sv[e];
+          o2[e] = u2[e] * cv[e] + u1[e] * sv[e];
         }
         T* dst = h < a.HQ
             ? qo + b * a.qo_s[0] + s * a.qo_s[1] + (int64_t)h * a.qo_s[2]
@@ -104,7 +134,7 @@ __device__ __forceinline__ void rope_token(const RopeArgs& a, int64_t b, int64_t
   }
 }
 
-template <typename T, int HALF>
+template <typename T, int HALF, bool VEC, bool QD>
 __global__ __launch_bounds__(kRopeWaves * kWave) void k_rope(const RopeArgs a) {
   __shared__ float cs[kRopeWaves][2][HALF];
   const int lane = threadIdx.x & 63;
@@ -156,19 +186,25 @@ __global__ __launch_bounds__(kRopeWaves * kWave) void k_rope(const RopeArgs a) {
     sv[0] = s0.x; sv[1] = s0.y; sv[2] = s0.z; sv[3] = s0.w;
     sv[4] = s1.x; sv[5] = s1.y; sv[6] = s1.z; sv[7] = s1.w;
   }
-  if (a.vec)
-    rope_token<true, T, HALF>(a, b, s, lane, cv, sv);
-  else
-    rope_token<false, T, HALF>(a, b, s, lane, cv, sv);
+  rope_token<VEC, QD, T, HALF>(a, b, s, lane, cv, sv);
+}
+
+template <typename T, int HALF>
+static void rope_variant(const RopeArgs& a, dim3 g, dim3 b, hipStream_t s) {
+  const bool qd = a.qd != nullptr;
+  if (a.vec && !qd) hipLaunchKernelGGL((k_rope<T, HALF, true, false>), g, b, 0, s, a);
+  else if (a.vec) hipLaunchKernelGGL((k_rope<T, HALF, true, true>), g, b, 0, s, a);
+  else if (!qd) hipLaunchKernelGGL((k_rope<T, HALF, false, false>), g, b, 0, s, a);
+  else hipLaunchKernelGGL((k_rope<T, HALF, false, true>), g, b, 0, s, a);
 }
 
 template <typename T>
 static hipError_t rope_half(const RopeArgs& a, int half, dim3 g, dim3 b, hipStream_t s, bool* sup) {
   *sup = true;
   switch (half) {
-    case 32: hipLaunchKernelGGL((k_rope<T, 32>), g, b, 0, s, a); break;
-    case 64: hipLaunchKernelGGL((k_rope<T, 64>), g, b, 0, s, a); break;
-    case 128: hipLaunchKernelGGL((k_rope<T, 128>), g, b, 0, s, a); break;
+    case 32: rope_variant<T, 32>(a, g, b, s); break;
+    case 64: rope_variant<T, 64>(a, g, b, s); break;
+    case 128: rope_variant<T, 128>(a, g, b, s); break;
     default: *sup = false; return hipErrorInvalidValue;
   }
   return hipGetLastError();

@@ -171,10 +171,11 @@ def rmsnorm_partials(rows, n):
 
 
 def rmsnorm_bwd(dys, x, w, eps, from_y=False, rstd=None, dr_out=None, slot=None, xs=None,
-                n_special=0, dr=None, dx=None, dw=None, name="_add_rmsnorm_bwd"):
+                n_special=0, dr=None, dx=None, dw=None, workspace=None, name="_add_rmsnorm_bwd"):
     """Backward of rmsnorm_fwd; see esep_rmsnorm_bwd. dys: list of [rows, n] tensors of one
     dtype (their sum is dy). dr: fp32 [rows, n] out; dx: low-precision [rows, n] out;
-    dw: [n] out (a [P, n] fp32 workspace is allocated here)."""
+    dw: [n] out, reduced through a [P, n] fp32 workspace (P = rmsnorm_partials(rows, n));
+    pass `workspace` to reuse one, else it is allocated here."""
     rows, n = x.shape
     dev = _dev(x, w, rstd, dr_out, slot, xs, dr, dx, dw, *dys)
     if len(dys) > 5:
@@ -196,7 +197,13 @@ def rmsnorm_bwd(dys, x, w, eps, from_y=False, rstd=None, dr_out=None, slot=None,
     n_part = 0
     if dw is not None:
         n_part = rmsnorm_partials(rows, n)
-        part = torch.empty((max(n_part, 1), n), device=dev, dtype=torch.float32)
+        if workspace is not None:
+            if (workspace.dtype != torch.float32 or not workspace.is_contiguous()
+                    or workspace.numel() < n_part * n or workspace.device != dev):
+                raise EsepError(f"workspace must be a contiguous fp32 tensor of >= {n_part}x{n}")
+            part = workspace
+        else:
+            part = torch.empty((max(n_part, 1), n), device=dev, dtype=torch.float32)
     arr = _VP5(*([d.data_ptr() for d in dys] + [None] * (5 - len(dys))))
     rc = lib().esep_rmsnorm_bwd(
         arr, len(dys), dtype_code(dys[0].dtype) if dys else 0, ld_dy,
