@@ -43,8 +43,11 @@ def round_bf16(x):
 
 
 def round_to(x, dtype):
-    """Round fp values to the storage dtype ('f32', 'f16', 'bf16'), returned as float64."""
+    """Round fp values to the storage dtype ('f32', 'f16', 'bf16'; 'f64' keeps them),
+    returned as float64."""
     x = np.asarray(x)
+    if dtype == "f64":
+        return x.astype(np.float64)
     if dtype == "f32":
         return x.astype(np.float32).astype(np.float64)
     if dtype == "f16":

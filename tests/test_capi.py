@@ -1,0 +1,107 @@
+"""The C ABI boundary without a GPU: libesep_body.so loads, exports every entry point that
+include/esep_body.h declares with the binding's signature, reports its ABI version, and
+rejects bad arguments before touching the device (negative status + message)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from solution.body import _hip
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "esep_body.h"
+
+
+def declared():
+    text = HEADER.read_text()
+    return re.findall(r"^(?:const char\*|int64_t|int)\s+(esep_\w+)\(", text, flags=re.M)
+
+
+def test_header_declares_the_binding_surface():
+    names = declared()
+    assert sorted(names) == sorted(_hip.SIGNATURES), names
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_hip.LIB_PATH))
+    for name in declared():
+        assert hasattr(lib, name), name
+
+
+def test_abi_version():
+    assert _hip.lib().esep_abi_version() == _hip.ABI_VERSION
+    m = re.search(r"#define ESEP_ABI_VERSION (\d+)", HEADER.read_text())
+    assert int(m.group(1)) == _hip.ABI_VERSION
+
+
+def _fwd(lib, **kw):
+    a = dict(x=1, x_dt=0, ld_x=8, delta=None, delta_dt=0, ld_d=0, w=1, r_out=None, ld_r=0,
+             y=1, y_dt=0, ld_y=8, rstd=None, slot=None, xs=None, k=0, rows=4, n=8, eps=1e-6,
+             stream=None)
+    a.update(kw)
+    return lib.esep_rmsnorm_fwd(*a.values())
+
+
+def test_rmsnorm_fwd_validation():
+    lib = _hip.lib()
+    assert _fwd(lib, n=0) == -2 and b"n=0" in lib.esep_last_error()
+    assert _fwd(lib, n=16385) == -2
+    assert _fwd(lib, rows=-1) == -2
+    assert _fwd(lib, x_dt=7) == -1
+    assert _fwd(lib, x=None) == -1
+    assert _fwd(lib, k=2) == -1 and b"n_special" in lib.esep_last_error()
+    assert _fwd(lib, ld_x=4) == -2
+    assert _fwd(lib, rows=0) == 0  # nothing to do, nothing launched
+    assert _fwd(lib, x=None, rows=0) == -1  # arguments are checked even for empty inputs
+
+
+def test_rmsnorm_bwd_validation():
+    lib = _hip.lib()
+    Arr = ctypes.c_void_p * 5
+
+    def bwd(**kw):
+        a = dict(dys=Arr(1), n_dy=1, dy_dt=2, ld_dy=8, dr_out=None, x=1, x_dt=2, ld_x=8, from_y=0,
+                 rstd=None, w=1, slot=None, xs=None, k=0, dr=None, dx=1, dx_dt=2, ld_out=8,
+                 part=None, n_part=0, dw=None, dw_dt=0, rows=4, n=8, eps=1e-6, stream=None)
+        a.update(kw)
+        return lib.esep_rmsnorm_bwd(*a.values())
+
+    assert bwd(n_dy=6) == -1
+    assert bwd(dys=Arr(None)) == -1
+    assert bwd(from_y=1) == -1 and b"rstd" in lib.esep_last_error()
+    assert bwd(dw=1) == -1  # no partials workspace
+    assert bwd(dw=1, part=1, n_part=3) == -2 and b"needs 1" in lib.esep_last_error()
+    assert bwd(rows=0) == 0
+
+
+def test_rope_validation():
+    lib = _hip.lib()
+    S3 = ctypes.c_int64 * 3
+    st = S3(0, 128, 128)
+
+    def rope(**kw):
+        a = dict(q=1, qs=st, qd=None, qds=None, k=1, ks=st, qo=1, qos=st, ko=1, kos=st, dt=1,
+                 B=1, S=4, HQ=1, HK=1, D=128, pos=None, pos_dt=0, pos_s=None, cu=None, n_seq=0,
+                 inv=1, sign=1.0, stream=None)
+        a.update(kw)
+        return lib.esep_rope(*a.values())
+
+    assert rope(D=96) == -2
+    assert rope(dt=5) == -1
+    assert rope(inv=None) == -1
+    assert rope(pos=1, pos_dt=3, pos_s=(ctypes.c_int64 * 2)(0, 1), cu=1, n_seq=1) == -1
+    assert rope(cu=1, n_seq=1, B=2) == -1
+    assert rope(HQ=0, HK=0) == -2
+    assert rope(S=0) == 0
+
+
+@pytest.mark.parametrize("rows,n", [(1, 1536), (37, 1536), (8192, 1536), (65536, 3584),
+                                    (4557, 1536), (100000, 24), (8192, 16384)])
+def test_partition_depends_on_shape_only(rows, n):
+    """The weight-gradient partition: at most 256 partial rows, every row covered, and a
+    pure function of (rows, n) (the C ABI takes no device argument)."""
+    p = _hip.rmsnorm_partials(rows, n)
+    assert 1 <= p <= 256 and p == _hip.rmsnorm_partials(rows, n)
+    assert _hip.rmsnorm_partials(0, n) == 0

@@ -1,0 +1,87 @@
+"""Host-side logic of the drop-in API without a GPU: exact-channel selection and its cache,
+the HF-exact inverse frequencies, and the rule that the kernels never fall back to a CPU
+path (CPU tensors are an error)."""
+
+import subprocess
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import norm_rope_ref as ref
+from solution.body import _hip, norm_rope
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def test_reference_constants():
+    """Names the reference's module exports (norm_rope.py:73, :113, :170)."""
+    assert norm_rope.MAX_DY == 5 and norm_rope.SPECIAL_W_MIN == 2.0 ** -10
+    assert norm_rope.NORM_BLOCK >= 3584  # the reference caps at 2048; config 5 needs 3584
+
+
+def test_inv_freq_matches_hf():
+    """Reference test_inv_freq_matches_hf (test_body_norm_rope.py:169-175): exact."""
+    from transformers import Qwen2Config
+    from transformers.models.qwen2.modeling_qwen2 import Qwen2RotaryEmbedding
+
+    cfg = Qwen2Config(hidden_size=1536, num_attention_heads=12, num_key_value_heads=2,
+                      rope_theta=1e6, max_position_embeddings=32768)
+    emb = Qwen2RotaryEmbedding(cfg)
+    torch.testing.assert_close(emb.inv_freq, norm_rope.default_inv_freq(128, 1e6), rtol=0, atol=0)
+
+
+def test_special_channels_matches_oracle_and_caches():
+    g = torch.Generator().manual_seed(0)
+    w = 1 + 0.1 * torch.randn(1536, generator=g)
+    w[[4, 90]] = 0.0
+    w[700] = 1e-5
+    slots, k = norm_rope.special_channels(w)
+    want, kk = ref.special_channels(w.numpy())
+    assert k == kk == 3 and np.array_equal(slots.numpy(), want)
+    assert norm_rope.special_channels(w)[0] is slots  # cached
+    w[5] = 0.0  # in-place edit bumps the version counter: recomputed
+    slots2, k2 = norm_rope.special_channels(w)
+    assert k2 == 4 and slots2[5].item() == 1
+
+
+def test_special_channels_threshold_read_at_call_time(monkeypatch):
+    w = torch.ones(64)
+    w[3] = 1e-4
+    assert norm_rope.special_channels(w)[1] == 1
+    monkeypatch.setattr(norm_rope, "SPECIAL_W_MIN", 0.0)
+    assert norm_rope.special_channels(w)[1] == 0
+
+
+def test_no_cpu_fallback():
+    """The kernels run on the device or not at all: CPU tensors raise EsepError."""
+    x = torch.randn(4, 64)
+    w = torch.ones(64)
+    with pytest.raises(_hip.EsepError):
+        norm_rope.rmsnorm(x, w)
+    with pytest.raises(_hip.EsepError):
+        norm_rope.add_rmsnorm(x, None, w, 1e-6, torch.float32)
+    q, k = torch.randn(4, 2, 64), torch.randn(4, 1, 64)
+    with pytest.raises(_hip.EsepError):
+        norm_rope.rope(q, k, torch.arange(4), norm_rope.default_inv_freq(64))
+
+
+def test_bench_refuses_several_gpus():
+    res = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"],
+                         capture_output=True, text=True, timeout=120)
+    assert res.returncode == 2 and "one GPU" in res.stderr
+
+
+def test_bench_byte_model_matches_baseline():
+    """Config 4's algorithmic bytes per step: 28 * (2 * 125.90 + 117.44) + 125.90 MB."""
+    import bench
+
+    c = bench.CFG4
+    T = c["B"] * c["S"]
+    norm = bench.norm_fwd_bytes(T, c["H"], 2, True) + bench.norm_bwd_bytes(T, c["H"], 2, True)
+    rope = 2 * bench.rope_bytes(T, c["HQ"], c["HK"], c["D"], 2)
+    assert round(norm / 1e6, 2) == 125.90 and round(rope / 1e6, 2) == 117.44
+    total = (2 * c["layers"] + 1) * norm + c["layers"] * rope
+    assert abs(total / 1e9 - 10.465) < 1e-3
