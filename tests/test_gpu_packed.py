@@ -1,0 +1,211 @@
+"""The packed-decoder patch point on the GPU: a tiny random Qwen2 through the patched
+Qwen2Model.forward (HIP norms and RoPE) against HF's original forward, restating the reference's
+solution/test_body_packed.py (:20-338): hidden states, loss and every gradient within the
+reference's tolerances, pad positions exactly zero, launch counts by kernel name, and the
+guarded fallbacks. peft / bitsandbytes are not installed, so the reference's "lora" and
+"nf4_lora" variants are replaced by "frozen" (only q/v projections train, as a LoRA run
+freezes the base model: frozen norm weights, no gradient into the embedding)."""
+
+import contextlib
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+LENS = [37, 20, 9, 30]
+L = 40
+VOCAB = 1000
+
+
+def _config():
+    from transformers import Qwen2Config
+
+    cfg = Qwen2Config(vocab_size=VOCAB, hidden_size=256, intermediate_size=512,
+                      num_hidden_layers=2, num_attention_heads=4, num_key_value_heads=2,
+                      head_dim=64, max_position_embeddings=1024, rms_norm_eps=1e-6,
+                      rope_theta=1e6, tie_word_embeddings=True, use_cache=False)
+    cfg._attn_implementation = "sdpa"
+    return cfg
+
+
+def _build(variant):
+    from transformers import Qwen2ForCausalLM
+
+    torch.manual_seed(0)
+    model = Qwen2ForCausalLM(_config())
+    with torch.no_grad():
+        for name, p in model.named_parameters():
+            if "norm" in name:
+                p.add_(0.1 * torch.randn_like(p))
+            elif name.endswith("bias"):
+                p.normal_(0, 0.1)
+    model = model.cuda().float()
+    if variant == "frozen":
+        for name, p in model.named_parameters():
+            p.requires_grad_(name.endswith(("q_proj.weight", "v_proj.weight")))
+    model.train()
+    return model
+
+
+def _batch(left=False):
+    g = torch.Generator().manual_seed(1)
+    ids = torch.randint(0, VOCAB, (len(LENS), L), generator=g)
+    mask = torch.zeros(len(LENS), L, dtype=torch.long)
+    for b, n in enumerate(LENS):
+        if left:
+            mask[b, L - n:] = 1
+        else:
+            mask[b, :n] = 1
+    ids[mask == 0] = 0
+    labels = ids.clone()
+    labels[mask == 0] = -100
+    labels[:, :3] = -100
+    if left:
+        for b, n in enumerate(LENS):
+            labels[b, L - n] = -100
+    return ids.cuda(), mask.cuda(), labels.cuda()
+
+
+@contextlib.contextmanager
+def _original_forward():
+    from transformers.models.qwen2 import modeling_qwen2
+
+    cls = modeling_qwen2.Qwen2Model
+    patched = cls.forward
+    cls.forward = patched.__wrapped__
+    try:
+        yield
+    finally:
+        cls.forward = patched
+
+
+def _run(model, ids, mask, labels, autocast=True, dtype=torch.float16):
+    model.zero_grad(set_to_none=True)
+    with torch.autocast("cuda", dtype=dtype, enabled=autocast):
+        out = model(input_ids=ids, attention_mask=mask, labels=labels, use_cache=False)
+        hidden = model.model(input_ids=ids, attention_mask=mask, use_cache=False).last_hidden_state
+    out.loss.backward()
+    grads = {n: p.grad.detach().float().clone() for n, p in model.named_parameters()
+             if p.requires_grad and p.grad is not None}
+    return {"hidden": hidden.detach().float(), "loss": out.loss.detach().float(), "grads": grads}
+
+
+def _rel(a, b):
+    return ((a - b).abs().max() / b.abs().max().clamp(min=1e-12)).item()
+
+
+def _compare(ref, new, mask, tol_h=5e-3, tol_loss=1e-3, tol_g=2e-2):
+    """Reference _compare (test_body_packed.py:216-232)."""
+    real = mask.bool()
+    assert set(new["grads"]) == set(ref["grads"]) and new["grads"]
+    assert torch.all(new["hidden"][~real] == 0)
+    assert _rel(new["hidden"][real], ref["hidden"][real]) < tol_h
+    assert abs((new["loss"] - ref["loss"]).item()) / abs(ref["loss"].item()) < tol_loss
+    worst = max(_rel(new["grads"][n], ref["grads"][n]) for n in ref["grads"])
+    assert worst < tol_g, worst
+
+
+def _counts(names):
+    return {k: names.count(k) for k in ("_add_rmsnorm_fwd", "_add_rmsnorm_bwd", "_rope_kernel")}
+
+
+@pytest.mark.parametrize("kernels", [True, False], ids=["kernels", "torch"])
+@pytest.mark.parametrize("left", [False, True], ids=["right_pad", "left_pad"])
+@pytest.mark.parametrize("variant", ["plain", "frozen"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+def test_packed_matches_original(variant, left, kernels, dtype):
+    from solution.body import _hip, packed, patch
+
+    patch()
+    model = _build(variant)
+    ids, mask, labels = _batch(left)
+    with _original_forward():
+        ref = _run(model, ids, mask, labels, dtype=dtype)
+    with packed.kernels_enabled(kernels), _hip.count_launches() as names:
+        new = _run(model, ids, mask, labels, dtype=dtype)
+    tol = dict(tol_h=5e-3, tol_loss=1e-3, tol_g=2e-2) if dtype == torch.float16 else \
+        dict(tol_h=3e-2, tol_loss=5e-3, tol_g=6e-2)
+    _compare(ref, new, mask, **tol)
+    n_layers = model.config.num_hidden_layers
+    c = _counts(names)
+    if kernels:
+        norms = 2 * n_layers + 1
+        # a frozen model gives the first norm no backward (its input needs no gradient)
+        norm_bwd = norms - (1 if variant == "frozen" else 0)
+        assert c["_add_rmsnorm_fwd"] == 2 * norms, c  # loss forward + hidden forward
+        assert c["_add_rmsnorm_bwd"] == norm_bwd, c
+        assert c["_rope_kernel"] == 3 * n_layers, c
+    else:
+        assert not any(c.values()), c
+
+
+def test_packed_kernels_pure_fp32():
+    """No autocast, fp32 model (reference :279-292): only summation order differs."""
+    from solution.body import _hip, patch
+
+    patch()
+    model = _build("plain")
+    ids, mask, labels = _batch()
+    with _original_forward():
+        ref = _run(model, ids, mask, labels, autocast=False)
+    with _hip.count_launches() as names:
+        new = _run(model, ids, mask, labels, autocast=False)
+    _compare(ref, new, mask, tol_h=1e-4, tol_loss=1e-5, tol_g=1e-3)
+    c = _counts(names)
+    assert c["_add_rmsnorm_fwd"] > 0 and c["_rope_kernel"] > 0, c
+
+
+def test_packed_fp16_residual_falls_back():
+    """A pure fp16 model keeps HF's norm rounding (reference :295-309): the norm kernel is not
+    used, RoPE still is; outputs match the original."""
+    from solution.body import _hip, patch
+
+    patch()
+    model = _build("frozen").half()
+    ids, mask, labels = _batch()
+    with _original_forward():
+        ref = _run(model, ids, mask, labels, autocast=False)
+    with _hip.count_launches() as names:
+        new = _run(model, ids, mask, labels, autocast=False)
+    _compare(ref, new, mask)
+    c = _counts(names)
+    assert c["_add_rmsnorm_fwd"] == 0 and c["_add_rmsnorm_bwd"] == 0, c
+    assert c["_rope_kernel"] > 0, c
+
+
+def test_fallbacks_match_original():
+    """No mask, a row without tokens, output_hidden_states and return_dict=False (reference
+    :312-338)."""
+    from solution.body import patch
+
+    patch()
+    model = _build("plain")
+    ids, mask, _ = _batch()
+    base = model.model
+    with torch.no_grad(), torch.autocast("cuda", dtype=torch.float16):
+        with _original_forward():
+            want = base(input_ids=ids, use_cache=False).last_hidden_state
+        got = base(input_ids=ids, use_cache=False).last_hidden_state
+        assert torch.equal(want, got)
+        empty = mask.clone()
+        empty[2] = 0
+        with _original_forward():
+            want = base(input_ids=ids, attention_mask=empty, use_cache=False).last_hidden_state
+        got = base(input_ids=ids, attention_mask=empty, use_cache=False).last_hidden_state
+        assert torch.equal(want, got)
+        out = base(input_ids=ids, attention_mask=mask, use_cache=False, output_hidden_states=True)
+        assert out.hidden_states is not None and len(out.hidden_states) == 3
+        tup = base(input_ids=ids, attention_mask=mask, use_cache=False, return_dict=False)
+        assert isinstance(tup, tuple) and tup[0].shape == (len(LENS), L, 256)
+
+
+def test_patch_is_idempotent():
+    from transformers.models.qwen2 import modeling_qwen2
+
+    from solution.body import patch
+
+    patch()
+    fwd = modeling_qwen2.Qwen2Model.forward
+    patch()
+    assert modeling_qwen2.Qwen2Model.forward is fwd and hasattr(fwd, "__wrapped__")
