@@ -38,6 +38,8 @@ for _p in (ROOT / "esep-soup-kernels_amd", ROOT):
 
 PEAK_GBS = 8000.0  # MI355X HBM3E, published
 CFG4 = dict(layers=28, B=8, S=1024, H=1536, HQ=12, HK=2, D=128, theta=1e6, eps=1e-6)
+# Config 5: large-token stress at Qwen2.5-7B-like width, varlen lengths U[128, 4096] (seed 0)
+CFG5 = dict(T=65536, H=3584, HQ=28, HK=4, D=128, theta=1e6, eps=1e-6, lo=128, hi=4096)
 
 
 def log(msg):
@@ -131,6 +133,111 @@ class Body:
         norm = norm_fwd_bytes(T, c["H"], e, self.save_rstd) + norm_bwd_bytes(T, c["H"], e, self.save_rstd)
         rope = 2 * rope_bytes(T, c["HQ"], c["HK"], c["D"], e)
         return (2 * L + 1) * norm + L * rope
+
+
+def config5_lengths(cfg):
+    """Sequence lengths U[lo, hi] drawn from seed 0 until T tokens (the last one truncated)."""
+    import torch
+
+    g = torch.Generator().manual_seed(0)
+    lens, total = [], 0
+    while total < cfg["T"]:
+        n = min(int(torch.randint(cfg["lo"], cfg["hi"] + 1, (1,), generator=g)), cfg["T"] - total)
+        lens.append(n)
+        total += n
+    return lens
+
+
+class Stress:
+    """Config 5: one RMSNorm (x [T, H] -> y, rstd; backward dx, dw) and one q/k RoPE on the
+    packed varlen layout with cu_seqlens (positions restart per sequence), forward + backward."""
+
+    def __init__(self, cfg, dev):
+        import torch
+
+        from solution.body import _hip
+
+        self.hip, self.cfg = _hip, cfg
+        T, H, HQ, HK, D = (cfg[k] for k in ("T", "H", "HQ", "HK", "D"))
+        bf = torch.bfloat16
+        g = torch.Generator(device=dev).manual_seed(5)
+
+        def rn(*shape):
+            return torch.randn(shape, generator=g, device=dev, dtype=torch.float32).to(bf)
+
+        self.lens = config5_lengths(cfg)
+        cu = [0]
+        for n in self.lens:
+            cu.append(cu[-1] + n)
+        self.cu = torch.tensor(cu, dtype=torch.int32, device=dev)
+        self.x, self.dy = rn(T, H), rn(T, H)
+        self.w = 1 + 0.02 * torch.randn(H, generator=g, device=dev)
+        self.y, self.dx = torch.empty(T, H, device=dev, dtype=bf), torch.empty(T, H, device=dev, dtype=bf)
+        self.rstd, self.dw = torch.empty(T, device=dev), torch.empty(H, device=dev)
+        self.ws = torch.empty(_hip.rmsnorm_partials(T, H), H, device=dev)
+        self.q, self.k = rn(1, T, HQ, D), rn(1, T, HK, D)
+        self.dqo, self.dko = rn(1, T, HQ, D), rn(1, T, HK, D)
+        self.qo, self.ko = torch.empty_like(self.q), torch.empty_like(self.k)
+        self.dq, self.dk = torch.empty_like(self.q), torch.empty_like(self.k)
+        self.inv_freq = (1.0 / (cfg["theta"] ** (torch.arange(0, D, 2, dtype=torch.float) / D))).to(dev)
+
+    def norm_fwd(self):
+        self.hip.rmsnorm_fwd(self.x, self.w, self.y, self.cfg["eps"], rstd=self.rstd)
+
+    def norm_bwd(self):
+        self.hip.rmsnorm_bwd([self.dy], self.x, self.w, self.cfg["eps"], rstd=self.rstd,
+                             dx=self.dx, dw=self.dw, workspace=self.ws)
+
+    def rope_fwd(self):
+        self.hip.rope(self.q, self.k, self.qo, self.ko, self.inv_freq, 1.0, cu_seqlens=self.cu)
+
+    def rope_bwd(self):
+        self.hip.rope(self.dqo, self.dko, self.dq, self.dk, self.inv_freq, -1.0, cu_seqlens=self.cu)
+
+    def step(self):
+        self.norm_fwd()
+        self.rope_fwd()
+        self.norm_bwd()
+        self.rope_bwd()
+
+    def kernel_bytes(self):
+        c = self.cfg
+        return {"rmsnorm_fwd": norm_fwd_bytes(c["T"], c["H"], 2, True),
+                "rmsnorm_bwd": norm_bwd_bytes(c["T"], c["H"], 2, True),
+                "rope_fwd": rope_bytes(c["T"], c["HQ"], c["HK"], c["D"], 2),
+                "rope_bwd": rope_bytes(c["T"], c["HQ"], c["HK"], c["D"], 2)}
+
+
+def run_config5(dev, steps):
+    """Times config 5 (graph replay) and each of its kernels; returns the JSON object."""
+    import torch
+
+    st = Stress(CFG5, dev)
+    torch.cuda.synchronize()
+    g = capture(st.step)
+    time_graph(g, 2)
+    ev_ms, wall_ms = time_graph(g, steps)
+    ms = max(ev_ms, wall_ms)
+    kb = st.kernel_bytes()
+    total = sum(kb.values())
+    kernels = {}
+    methods = {"rmsnorm_fwd": st.norm_fwd, "rmsnorm_bwd": st.norm_bwd, "rope_fwd": st.rope_fwd,
+               "rope_bwd": st.rope_bwd}
+    for name in kb:
+        kg = capture(methods[name])
+        time_graph(kg, 2)
+        kms, _ = time_graph(kg, steps)
+        kernels[name] = {"us": round(kms * 1e3, 2), "GB/s": round(kb[name] / (kms * 1e-3) / 1e9, 1)}
+    gbs = total / (ms * 1e-3) / 1e9
+    log(f"config 5: {ms:.3f} ms per fwd+bwd, {gbs:.0f} GB/s = {gbs / PEAK_GBS:.1%} of peak")
+    del st, g
+    torch.cuda.empty_cache()
+    return {"workload": "config5: T=65536 packed (29 sequences, lengths U[128,4096] seed 0, "
+                        "cu_seqlens), H=3584, HQ=28, HK=4, D=128, bf16; RMSNorm + q/k RoPE "
+                        "forward + backward (dx, dw, dq, dk)",
+            "ms_per_step": round(ms, 4), "GB/s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4),
+            "tokens_per_s": round(CFG5["T"] / (ms * 1e-3), 1), "bytes_per_step": total,
+            "kernels": kernels}
 
 
 def capture(fn, warm=True):
@@ -243,6 +350,11 @@ def main():
     ap.add_argument("--rstd", choices=["saved", "recomputed"], default="saved")
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--kernel-reps", type=int, default=20)
+    ap.add_argument("--no-config5", action="store_true", help="skip the config 5 stress line")
+    ap.add_argument("--pmc-kernel", choices=["rmsnorm_fwd", "rmsnorm_bwd", "rope_fwd", "rope_bwd"],
+                    help="counter-collection run: a calibration copy of 256 MiB (read 256 MiB, "
+                         "write 256 MiB) three times, then one launch per layer of this kernel "
+                         "at config 4; no timing, no JSON (for rocprofv3 --pmc)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py measures one GPU: this build has no multi-GPU path (--gpus {args.gpus} "
@@ -262,6 +374,24 @@ def main():
     log(f"allocating config 4 ({cfg['layers']} layers, T={cfg['B'] * cfg['S']}) on {torch.cuda.get_device_name(dev)}")
     body = Body(cfg, save_rstd, dev)
     torch.cuda.synchronize()
+    if args.pmc_kernel:
+        src = torch.ones(128 << 20, device=dev, dtype=torch.bfloat16)  # 256 MiB
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        L = cfg["layers"]
+        if args.pmc_kernel.startswith("rmsnorm"):
+            fn = body.norm_fwd if args.pmc_kernel == "rmsnorm_fwd" else body.norm_bwd
+            for i in range(2 * L + 1):
+                fn(i)
+        else:
+            fn = body.rope_fwd if args.pmc_kernel == "rope_fwd" else body.rope_bwd
+            for l in range(L):
+                fn(l)
+        torch.cuda.synchronize()
+        log(f"pmc run done: {args.pmc_kernel}")
+        return 0
     log("capturing the step graph")
     g = capture(body.step)
     for _ in range(args.warmup):
@@ -282,6 +412,11 @@ def main():
                 "us_per_launch": round(us, 3), "bytes_per_launch": nbytes,
                 "all_kernels": {k: {"us": round(v[0], 3), "GB/s": round(v[1] / (v[0] * 1e-6) / 1e9, 1),
                                     "launches_per_step": v[2]} for k, v in kr.items()}}
+
+    del g
+    del body
+    torch.cuda.empty_cache()
+    c5 = None if args.no_config5 else run_config5(dev, max(args.steps // 3, 5))
 
     cpu = None
     if not args.no_cpu:
@@ -307,6 +442,7 @@ def main():
         "ms_per_step_events": round(ev_ms, 4),
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "config5": c5,
     }
     print(json.dumps(out), flush=True)
     return 0

@@ -205,7 +205,9 @@ int esep_rmsnorm_bwd(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
   int wpr, nv;
   norm_shape(n, &wpr, &nv);
   a.wpr = wpr;
-  const int gpb = bwd_groups(wpr);
+  // Without a weight gradient every row group owns one row and small blocks (4 row groups of
+  // one wavefront, or one group of wpr wavefronts) let finished waves be replaced one by one.
+  const int gpb = dw ? bwd_groups(wpr) : (wpr >= 4 ? 1 : 4 / wpr);
   int64_t blocks;
   if (dw) {
     int64_t P, rpb;

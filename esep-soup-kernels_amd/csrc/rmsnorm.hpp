@@ -402,6 +402,7 @@ __device__ __forceinline__ void bwd_rows_fast(const BwdArgs& a, float* red, floa
   const int iters = (int)((a.rpb + gpb - 1) / gpb);
   const bool want_dw = a.part != nullptr;
   const Span rw = make_span(a.w, (uint32_t)n * 4u);
+  const float inv_n = 1.0f / (float)n;
   const int stride = NV * G * 8;
   float* acc = lds + grp * stride;
   if (want_dw) {
@@ -482,7 +483,7 @@ __device__ __forceinline__ void bwd_rows_fast(const BwdArgs& a, float* red, floa
         p = fmaf(dy[k][e], x[k][e], p);
       }
     }
-    const float proj = row_sum(p, a.wpr, red) / (float)n;
+    const float proj = row_sum(p, a.wpr, red) * inv_n;
 #pragma unroll
     for (int k = 0; k < NV; ++k)
 #pragma unroll
@@ -528,12 +529,12 @@ __global__ __launch_bounds__(kBwdThreads) void k_rmsnorm_bwd(const BwdArgs a) {
     bwd_rows<NV, VEC, TX, TDY, TO>(a, red, lds);
 }
 
-// Stage 2 of the weight gradient: dw[j] = sum_p part[p, j]. A block of 256 threads owns 32
-// columns: thread (stripe r = tid / 8, quad c = tid % 8) adds the 4 columns 4c..4c+3 of rows
-// p = r, r + 32, r + 64, ... in ascending p (eight 16-byte loads in flight), then the 32 stripe
-// sums are added in stripe order. n % 4 != 0 takes the same order one column at a time.
-constexpr int kRedCols = 32;
-constexpr int kRedStripes = 32;
+// Stage 2 of the weight gradient: dw[j] = sum_p part[p, j]. A block of 256 threads owns 16
+// columns: thread (stripe r = tid / 4, quad c = tid % 4) adds the 4 columns 4c..4c+3 of rows
+// p = r, r + 64, r + 128, ... in ascending p, then a fixed 6-level tree adds the 64 stripe
+// sums (stripe r + h into stripe r). n % 4 != 0 takes the same order one column at a time.
+constexpr int kRedCols = 16;
+constexpr int kRedStripes = 64;
 
 template <typename TW>
 __global__ __launch_bounds__(256) void k_dgamma_reduce(const float* __restrict__ part,
@@ -545,7 +546,7 @@ __global__ __launch_bounds__(256) void k_dgamma_reduce(const float* __restrict__
   f32x4 s = {0.f, 0.f, 0.f, 0.f};
   if ((n & 3) == 0) {
     if (j < n) {
-#pragma unroll 8
+#pragma unroll 4
       for (int64_t p = r; p < P; p += kRedStripes)
         s += *reinterpret_cast<const f32x4*>(part + p * n + j);
     }
@@ -560,10 +561,13 @@ __global__ __launch_bounds__(256) void k_dgamma_reduce(const float* __restrict__
   }
   red[r][c] = s;
   __syncthreads();
-  if (r == 0) {
-    f32x4 t = red[0][c];
 #pragma unroll
-    for (int i = 1; i < kRedStripes; ++i) t += red[i][c];
+  for (int h = kRedStripes / 2; h >= 1; h >>= 1) {
+    if (r < h) red[r][c] += red[r + h][c];
+    __syncthreads();
+  }
+  if (r == 0) {
+    const f32x4 t = red[0][c];
     const float v[4] = {t.x, t.y, t.z, t.w};
 #pragma unroll
     for (int e = 0; e < 4; ++e)
