@@ -407,8 +407,14 @@ def main():
     kr = kernel_rooflines(body, args.kernel_reps)
     name, (us, nbytes, n) = max(kr.items(), key=lambda kv: kv[1][0] * kv[1][2])
     achieved = nbytes / (us * 1e-6) / 1e9
+    # HBM bytes per launch measured by rocprofv3 FETCH_SIZE / WRITE_SIZE runs (bench.py
+    # --pmc-kernel), each scaled by the counter's reading on a 256 MiB copy
+    traffic = None
+    tpath = ROOT / "profiles" / "hbm_traffic_config4.json"
+    if tpath.exists() and save_rstd:
+        traffic = json.loads(tpath.read_text()).get(name, {}).get("traffic_bytes")
     roofline = {"bound": "hbm", "achieved": round(achieved, 1), "peak": PEAK_GBS, "unit": "GB/s",
-                "frac": round(achieved / PEAK_GBS, 4), "traffic": None, "kernel": name,
+                "frac": round(achieved / PEAK_GBS, 4), "traffic": traffic, "kernel": name,
                 "us_per_launch": round(us, 3), "bytes_per_launch": nbytes,
                 "all_kernels": {k: {"us": round(v[0], 3), "GB/s": round(v[1] / (v[0] * 1e-6) / 1e9, 1),
                                     "launches_per_step": v[2]} for k, v in kr.items()}}
