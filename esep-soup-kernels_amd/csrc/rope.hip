@@ -1,6 +1,6 @@
 // Rotary embedding (forward and backward) on q and k for gfx950 (MI355X).
 //
-// Mapping. One wavefront per token. The token's D/2 angles are computed once: lane j takes
+// Mapping. One wavefront per token (two on the vector path, processed together). The token's D/2 angles are computed once: lane j takes
 // angle j (and j + 64 for D = 256), calls the accurate sincosf (full range reduction, so
 // positions in the tens of thousands stay exact to fp32 rounding) and parks cos / sin in a
 // per-wave LDS slot. Each lane then owns 8 consecutive frequencies of a head half, reads their
@@ -67,89 +67,14 @@ __device__ __forceinline__ void st_half(T* p, const float (&v)[8]) {
   }
 }
 
-template <bool VEC, bool QD, typename T, int HALF>
-__device__ __forceinline__ void rope_token(const RopeArgs& a, int64_t b, int64_t s, int lane,
-                                           const float (&cv)[8], const float (&sv)[8]) {
-  constexpr int LPH = HALF / 8;
-  constexpr int HPP = kWave / LPH;
-  const int c = lane % LPH;
-  const int hs = lane / LPH;
-  const int nh = a.HQ + a.HK;
-  const T* __restrict__ q = static_cast<const T*>(a.q);
-  const T* __restrict__ qd = static_cast<const T*>(a.qd);
-  const T* __restrict__ k = static_cast<const T*>(a.k);
-  T* __restrict__ qo = static_cast<T*>(a.qo);
-  T* __restrict__ ko = static_cast<T*>(a.ko);
-
-  for (int h0 = 0; h0 < nh; h0 += kRopePasses * HPP) {
-    // Issue every load of up to four passes of heads (raw, packed) before any rotation.
-    Raw<T> x1[kRopePasses], x2[kRopePasses], d1[kRopePasses], d2[kRopePasses];
-#pragma unroll
-    for (int i = 0; i < kRopePasses; ++i) {
-      const int h = h0 + i * HPP + hs;
-      if (h < nh) {
-        const T* src = h < a.HQ
-            ? q + b * a.q_s[0] + s * a.q_s[1] + (int64_t)h * a.q_s[2]
-            : k + b * a.k_s[0] + s * a.k_s[1] + (int64_t)(h - a.HQ) * a.k_s[2];
-        x1[i] = ld_raw<VEC>(src + 8 * c);
-        x2[i] = ld_raw<VEC>(src + HALF + 8 * c);
-        if (QD && h < a.HQ) {
-          const T* dsrc = qd + b * a.qd_s[0] + s * a.qd_s[1] + (int64_t)h * a.qd_s[2];
-          d1[i] = ld_raw<VEC>(dsrc + 8 * c);
-          d2[i] = ld_raw<VEC>(dsrc + HALF + 8 * c);
-        }
-      }
-    }
-#pragma unroll
-    for (int i = 0; i < kRopePasses; ++i) {
-      const int h = h0 + i * HPP + hs;
-      if (h < nh) {
-        float u1[8], u2[8];
-        Buf<T>::unpack(x1[i], u1);
-        Buf<T>::unpack(x2[i], u2);
-        if (QD && h < a.HQ) {
-          // q + q_delta in the storage dtype (one rounding), as the unfused model adds them
-          float e1[8], e2[8];
-          Buf<T>::unpack(d1[i], e1);
-          Buf<T>::unpack(d2[i], e2);
-#pragma unroll
-          for (int e = 0; e < 8; ++e) {
-            u1[e] = Elt<T>::round(u1[e] + e1[e]);
-            u2[e] = Elt<T>::round(u2[e] + e2[e]);
-          }
-        }
-        float o1[8], o2[8];
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          o1[e] = u1[e] * cv[e] - u2[e] * sv[e];
-          o2[e] = u2[e] * cv[e] + u1[e] * sv[e];
-        }
-        T* dst = h < a.HQ
-            ? qo + b * a.qo_s[0] + s * a.qo_s[1] + (int64_t)h * a.qo_s[2]
-            : ko + b * a.ko_s[0] + s * a.ko_s[1] + (int64_t)(h - a.HQ) * a.ko_s[2];
-        st_half<VEC>(dst + 8 * c, o1);
-        st_half<VEC>(dst + HALF + 8 * c, o2);
-      }
-    }
-  }
-}
-
-template <typename T, int HALF, bool VEC, bool QD>
-__global__ __launch_bounds__(kRopeWaves * kWave) void k_rope(const RopeArgs a) {
-  __shared__ float cs[kRopeWaves][2][HALF];
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int64_t t = (int64_t)blockIdx.x * kRopeWaves + wave;
-  if (t >= a.B * a.S) return;  // whole wavefront leaves; nothing below waits on other waves
-  const int64_t b = t / a.S;
-  const int64_t s = t - b * a.S;
-
-  int64_t pos;
+// Position of token (b, s): explicit, from cu_seqlens, or s itself.
+__device__ __forceinline__ int64_t token_pos(const RopeArgs& a, int64_t b, int64_t s, int lane) {
   if (a.pos != nullptr) {
     const int64_t off = b * a.pos_s[0] + s * a.pos_s[1];
-    pos = a.pos_i64 ? static_cast<const int64_t*>(a.pos)[off]
-                    : (int64_t) static_cast<const int32_t*>(a.pos)[off];
-  } else if (a.cu != nullptr) {
+    return a.pos_i64 ? static_cast<const int64_t*>(a.pos)[off]
+                     : (int64_t) static_cast<const int32_t*>(a.pos)[off];
+  }
+  if (a.cu != nullptr) {
     // Sequence of token s: the number of starts cu[1..n_seq-1] that are <= s (cu is
     // non-decreasing; empty sequences are skipped over), counted 64 starts at a time.
     int idx = 0;
@@ -159,63 +84,170 @@ __global__ __launch_bounds__(kRopeWaves * kWave) void k_rope(const RopeArgs a) {
       idx += __popcll(__ballot(le));
       if (base + kWave >= a.n_seq || (int64_t)a.cu[base + kWave - 1] > s) break;
     }
-    pos = s - (int64_t)a.cu[idx];
-  } else {
-    pos = s;
+    return s - (int64_t)a.cu[idx];
   }
+  return s;
+}
 
-  const float p = (float)pos;
-  for (int j = lane; j < HALF; j += kWave) {
-    const float ang = p * a.inv_freq[j];
-    float sn, cn;
-    sincosf(ang, &sn, &cn);
-    cs[wave][0][j] = cn;
-    cs[wave][1][j] = sn * a.sign;
+// The TPW tokens of one wavefront. Heads go in groups of PG passes per token (TPW * PG = 4
+// passes in total); each group issues every load of every token before any rotation.
+template <bool VEC, bool QD, typename T, int HALF, int TPW>
+__device__ __forceinline__ void rope_tokens(const RopeArgs& a, const int64_t (&bb)[TPW],
+                                            const int64_t (&ss)[TPW], const bool (&live)[TPW],
+                                            int lane, const float (&cv)[TPW][8],
+                                            const float (&sv)[TPW][8]) {
+  constexpr int LPH = HALF / 8;
+  constexpr int HPP = kWave / LPH;
+  constexpr int PG = kRopePasses / TPW;
+  const int c = lane % LPH;
+  const int hs = lane / LPH;
+  const int nh = a.HQ + a.HK;
+  const T* __restrict__ q = static_cast<const T*>(a.q);
+  const T* __restrict__ qd = static_cast<const T*>(a.qd);
+  const T* __restrict__ k = static_cast<const T*>(a.k);
+  T* __restrict__ qo = static_cast<T*>(a.qo);
+  T* __restrict__ ko = static_cast<T*>(a.ko);
+
+  for (int h0 = 0; h0 < nh; h0 += PG * HPP) {
+    Raw<T> x1[TPW][PG], x2[TPW][PG], d1[TPW][PG], d2[TPW][PG];
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+#pragma unroll
+      for (int i = 0; i < PG; ++i) {
+        const int h = h0 + i * HPP + hs;
+        if (live[t] && h < nh) {
+          const T* src = h < a.HQ
+              ? q + bb[t] * a.q_s[0] + ss[t] * a.q_s[1] + (int64_t)h * a.q_s[2]
+              : k + bb[t] * a.k_s[0] + ss[t] * a.k_s[1] + (int64_t)(h - a.HQ) * a.k_s[2];
+          x1[t][i] = ld_raw<VEC>(src + 8 * c);
+          x2[t][i] = ld_raw<VEC>(src + HALF + 8 * c);
+          if (QD && h < a.HQ) {
+            const T* dsrc = qd + bb[t] * a.qd_s[0] + ss[t] * a.qd_s[1] + (int64_t)h * a.qd_s[2];
+            d1[t][i] = ld_raw<VEC>(dsrc + 8 * c);
+            d2[t][i] = ld_raw<VEC>(dsrc + HALF + 8 * c);
+          }
+        }
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+#pragma unroll
+      for (int i = 0; i < PG; ++i) {
+        const int h = h0 + i * HPP + hs;
+        if (live[t] && h < nh) {
+          float u1[8], u2[8];
+          Buf<T>::unpack(x1[t][i], u1);
+          Buf<T>::unpack(x2[t][i], u2);
+          if (QD && h < a.HQ) {
+            // q + q_delta in the storage dtype (one rounding), as the unfused model adds them
+            float e1[8], e2[8];
+            Buf<T>::unpack(d1[t][i], e1);
+            Buf<T>::unpack(d2[t][i], e2);
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+              u1[e] = Elt<T>::round(u1[e] + e1[e]);
+              u2[e] = Elt<T>::round(u2[e] + e2[e]);
+            }
+          }
+          float o1[8], o2[8];
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            o1[e] = u1[e] * cv[t][e] - u2[e] * sv[t][e];
+            o2[e] = u2[e] * cv[t][e] + u1[e] * sv[t][e];
+          }
+          T* dst = h < a.HQ
+              ? qo + bb[t] * a.qo_s[0] + ss[t] * a.qo_s[1] + (int64_t)h * a.qo_s[2]
+              : ko + bb[t] * a.ko_s[0] + ss[t] * a.ko_s[1] + (int64_t)(h - a.HQ) * a.ko_s[2];
+          st_half<VEC>(dst + 8 * c, o1);
+          st_half<VEC>(dst + HALF + 8 * c, o2);
+        }
+      }
+    }
+  }
+}
+
+template <typename T, int HALF, bool VEC, bool QD, int TPW>
+__global__ __launch_bounds__(kRopeWaves * kWave) void k_rope(const RopeArgs a) {
+  __shared__ float cs[kRopeWaves][TPW][2][HALF];
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int64_t tokens = a.B * a.S;
+  const int64_t t0 = ((int64_t)blockIdx.x * kRopeWaves + wave) * TPW;
+  if (t0 >= tokens) return;  // whole wavefront leaves; nothing below waits on other waves
+  int64_t bb[TPW], ss[TPW];
+  bool live[TPW];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    live[t] = t0 + t < tokens;
+    const int64_t tt = live[t] ? t0 + t : t0;
+    bb[t] = tt / a.S;
+    ss[t] = tt - bb[t] * a.S;
+    const float p = (float)token_pos(a, bb[t], ss[t], lane);
+    for (int j = lane; j < HALF; j += kWave) {
+      const float ang = p * a.inv_freq[j];
+      float sn, cn;
+      sincosf(ang, &sn, &cn);
+      cs[wave][t][0][j] = cn;
+      cs[wave][t][1][j] = sn * a.sign;
+    }
   }
   wave_lds_sync();
   constexpr int LPH = HALF / 8;
   const int c = lane % LPH;
-  float cv[8], sv[8];
-  {
-    const f32x4 c0 = *reinterpret_cast<const f32x4*>(&cs[wave][0][8 * c]);
-    const f32x4 c1 = *reinterpret_cast<const f32x4*>(&cs[wave][0][8 * c + 4]);
-    const f32x4 s0 = *reinterpret_cast<const f32x4*>(&cs[wave][1][8 * c]);
-    const f32x4 s1 = *reinterpret_cast<const f32x4*>(&cs[wave][1][8 * c + 4]);
-    cv[0] = c0.x; cv[1] = c0.y; cv[2] = c0.z; cv[3] = c0.w;
-    cv[4] = c1.x; cv[5] = c1.y; cv[6] = c1.z; cv[7] = c1.w;
-    sv[0] = s0.x; sv[1] = s0.y; sv[2] = s0.z; sv[3] = s0.w;
-    sv[4] = s1.x; sv[5] = s1.y; sv[6] = s1.z; sv[7] = s1.w;
+  float cv[TPW][8], sv[TPW][8];
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
+    const f32x4 c0 = *reinterpret_cast<const f32x4*>(&cs[wave][t][0][8 * c]);
+    const f32x4 c1 = *reinterpret_cast<const f32x4*>(&cs[wave][t][0][8 * c + 4]);
+    const f32x4 s0 = *reinterpret_cast<const f32x4*>(&cs[wave][t][1][8 * c]);
+    const f32x4 s1 = *reinterpret_cast<const f32x4*>(&cs[wave][t][1][8 * c + 4]);
+    cv[t][0] = c0.x; cv[t][1] = c0.y; cv[t][2] = c0.z; cv[t][3] = c0.w;
+    cv[t][4] = c1.x; cv[t][5] = c1.y; cv[t][6] = c1.z; cv[t][7] = c1.w;
+    sv[t][0] = s0.x; sv[t][1] = s0.y; sv[t][2] = s0.z; sv[t][3] = s0.w;
+    sv[t][4] = s1.x; sv[t][5] = s1.y; sv[t][6] = s1.z; sv[t][7] = s1.w;
   }
-  rope_token<VEC, QD, T, HALF>(a, b, s, lane, cv, sv);
+  rope_tokens<VEC, QD, T, HALF, TPW>(a, bb, ss, live, lane, cv, sv);
 }
 
+// Tokens per wavefront: two when a token's heads fit in at most two passes (each lane then
+// keeps both tokens' loads in flight at once), else one (its four passes already do).
 template <typename T, int HALF>
-static void rope_variant(const RopeArgs& a, dim3 g, dim3 b, hipStream_t s) {
+static void rope_variant(const RopeArgs& a, hipStream_t s) {
+  constexpr int HPP = kWave / (HALF / 8);
   const bool qd = a.qd != nullptr;
-  if (a.vec && !qd) hipLaunchKernelGGL((k_rope<T, HALF, true, false>), g, b, 0, s, a);
-  else if (a.vec) hipLaunchKernelGGL((k_rope<T, HALF, true, true>), g, b, 0, s, a);
-  else if (!qd) hipLaunchKernelGGL((k_rope<T, HALF, false, false>), g, b, 0, s, a);
-  else hipLaunchKernelGGL((k_rope<T, HALF, false, true>), g, b, 0, s, a);
+  const int64_t tokens = a.B * a.S;
+  const int passes = (a.HQ + a.HK + HPP - 1) / HPP;
+  const int tpw = (a.vec && passes <= 2) ? 2 : 1;
+  const dim3 b(kRopeWaves * kWave);
+  const dim3 g((unsigned)((tokens + kRopeWaves * tpw - 1) / (kRopeWaves * tpw)));
+  if (a.vec) {
+    if (tpw == 2 && !qd) hipLaunchKernelGGL((k_rope<T, HALF, true, false, 2>), g, b, 0, s, a);
+    else if (tpw == 2) hipLaunchKernelGGL((k_rope<T, HALF, true, true, 2>), g, b, 0, s, a);
+    else if (!qd) hipLaunchKernelGGL((k_rope<T, HALF, true, false, 1>), g, b, 0, s, a);
+    else hipLaunchKernelGGL((k_rope<T, HALF, true, true, 1>), g, b, 0, s, a);
+  } else if (!qd) {
+    hipLaunchKernelGGL((k_rope<T, HALF, false, false, 1>), g, b, 0, s, a);
+  } else {
+    hipLaunchKernelGGL((k_rope<T, HALF, false, true, 1>), g, b, 0, s, a);
+  }
 }
 
 template <typename T>
-static hipError_t rope_half(const RopeArgs& a, int half, dim3 g, dim3 b, hipStream_t s, bool* sup) {
+static hipError_t rope_half(const RopeArgs& a, int half, hipStream_t s, bool* sup) {
   *sup = true;
   switch (half) {
-    case 32: rope_variant<T, 32>(a, g, b, s); break;
-    case 64: rope_variant<T, 64>(a, g, b, s); break;
-    case 128: rope_variant<T, 128>(a, g, b, s); break;
+    case 32: rope_variant<T, 32>(a, s); break;
+    case 64: rope_variant<T, 64>(a, s); break;
+    case 128: rope_variant<T, 128>(a, s); break;
     default: *sup = false; return hipErrorInvalidValue;
   }
   return hipGetLastError();
 }
 
 hipError_t launch_rope(const RopeArgs& a, int dt, int half, hipStream_t s, bool* sup) {
-  const int64_t tokens = a.B * a.S;
-  const dim3 grid((unsigned)((tokens + kRopeWaves - 1) / kRopeWaves)), block(kRopeWaves * kWave);
-  if (dt == 0) return rope_half<float>(a, half, grid, block, s, sup);
-  if (dt == 1) return rope_half<_Float16>(a, half, grid, block, s, sup);
-  if (dt == 2) return rope_half<__bf16>(a, half, grid, block, s, sup);
+  if (dt == 0) return rope_half<float>(a, half, s, sup);
+  if (dt == 1) return rope_half<_Float16>(a, half, s, sup);
+  if (dt == 2) return rope_half<__bf16>(a, half, s, sup);
   *sup = false;
   return hipErrorInvalidValue;
 }
