@@ -57,18 +57,16 @@ size_t bwd_tree_lds(int gpb, int nv, int wpr) {
   return (size_t)slots * (size_t)nv * 64 * (size_t)wpr * 8 * sizeof(float);
 }
 
-// Rows-per-block partition of the backward pass with a weight gradient: P blocks of rpb
-// contiguous rows, at most 256 blocks, at least one row per row group. Only (rows, n) enter.
-void bwd_partition(int64_t rows, int64_t n, int64_t* P, int64_t* rpb) {
+// Block count P of the backward pass with a weight gradient (= rows of the [P, n] partials):
+// one block per gpb rows, at most 256 (one 1024-thread block per CU), at least 1. Only
+// (rows, n) enter, so the weight-gradient summation order is fixed for a shape.
+int64_t bwd_partials(int64_t rows, int64_t n) {
   int wpr, nv;
   norm_shape(n, &wpr, &nv);
   const int64_t gpb = bwd_groups(wpr);
   int64_t p = (rows + gpb - 1) / gpb;
   if (p > 256) p = 256;
-  if (p < 1) p = 1;
-  const int64_t r = (rows + p - 1) / p;
-  *rpb = r;
-  *P = (rows + r - 1) / r;
+  return p < 1 ? 1 : p;
 }
 
 }  // namespace
@@ -141,9 +139,7 @@ int esep_rmsnorm_fwd(const void* x, int x_dt, int64_t ld_x, const void* delta, i
 
 int64_t esep_rmsnorm_partials(int64_t rows, int64_t n) {
   if (rows <= 0 || n < 1 || n > ESEP_NORM_MAX_COLS) return 0;
-  int64_t P, rpb;
-  bwd_partition(rows, n, &P, &rpb);
-  return P;
+  return bwd_partials(rows, n);
 }
 
 int esep_rmsnorm_bwd(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
@@ -208,16 +204,7 @@ int esep_rmsnorm_bwd(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
   // Without a weight gradient every row group owns one row and small blocks (4 row groups of
   // one wavefront, or one group of wpr wavefronts) let finished waves be replaced one by one.
   const int gpb = dw ? bwd_groups(wpr) : (wpr >= 4 ? 1 : 4 / wpr);
-  int64_t blocks;
-  if (dw) {
-    int64_t P, rpb;
-    bwd_partition(rows, n, &P, &rpb);
-    a.rpb = rpb;
-    blocks = P;
-  } else {
-    a.rpb = gpb;
-    blocks = (rows + gpb - 1) / gpb;
-  }
+  const int64_t blocks = dw ? bwd_partials(rows, n) : (rows + gpb - 1) / gpb;
   if (blocks > 0x7fffffff) return fail(ESEP_ESHAPE, "rmsnorm_bwd: too many rows");
 
   const int xdt = n_dy > 0 ? x_dt : ESEP_F32;

@@ -13,11 +13,14 @@
 // wavefronts add their wave sums through LDS in wave order. Everything is reproducible run
 // to run.
 //
-// Weight gradient (backward): the rows are split into P contiguous blocks of rpb rows, P and
-// rpb depending on (rows, n) only (esep_rmsnorm_partials). Each lane accumulates dy * xhat of
-// its chunks in fp32 registers over the rows its group handles, the groups of a block are
-// combined by a fixed LDS tree, and the block writes one fp32 row of the [P, n] partials.
-// A second kernel sums the partials over P in a fixed order. No atomics anywhere.
+// Weight gradient (backward): a grid of P blocks (P depends on (rows, n) only,
+// esep_rmsnorm_partials) deals the rows out grid-strided: row group g of block b takes rows
+// (b + i * P) * gpb + g for i = 0, 1, ..., so the rows in flight at any moment are one
+// contiguous stretch of memory (contiguous per-block ranges put P streams a fixed stride apart,
+// which measured 8% slower on HBM). Each lane accumulates dy * xhat of its chunks in fp32 over
+// the rows of its group, the groups of a block are combined in a fixed order, and the block
+// writes one fp32 row of the [P, n] partials. A second kernel sums the partials over P in a
+// fixed order. No atomics anywhere: the result depends on (rows, n) and the data only.
 #pragma once
 
 #include <type_traits>
@@ -62,7 +65,6 @@ struct BwdArgs {
   int64_t ld_out;
   float* part;  // [P, n] weight-gradient partials or nullptr
   int64_t rows;
-  int64_t rpb;  // rows per block
   int n;
   float eps;
   int wpr;
@@ -237,9 +239,9 @@ __device__ __forceinline__ void bwd_rows(const BwdArgs& a, float* red, float* ld
   const int grp = wave_id() / a.wpr;
   const int tg = (int)threadIdx.x - grp * G;
   const int n = a.n;
-  const int64_t start = (int64_t)blockIdx.x * a.rpb;
-  const int64_t end = start + a.rpb < a.rows ? start + a.rpb : a.rows;
-  const int iters = (int)((a.rpb + gpb - 1) / gpb);
+  const int64_t step = (int64_t)gridDim.x * gpb;  // grid-strided rows
+  const int64_t first = (int64_t)blockIdx.x * gpb + grp;
+  const int iters = (int)((a.rows + step - 1) / step);
   const bool want_dw = a.part != nullptr;
   const Span rw = make_span(a.w, (uint32_t)n * 4u);
 
@@ -250,8 +252,8 @@ __device__ __forceinline__ void bwd_rows(const BwdArgs& a, float* red, float* ld
     for (int e = 0; e < 8; ++e) acc[k][e] = 0.f;
 
   for (int it = 0; it < iters; ++it) {
-    const int64_t row = start + grp + (int64_t)it * gpb;
-    const bool ok = row < end;
+    const int64_t row = first + (int64_t)it * step;
+    const bool ok = row < a.rows;
     float dr[NV][8];
 
     if (a.n_dy > 0) {
@@ -397,9 +399,9 @@ __device__ __forceinline__ void bwd_rows_fast(const BwdArgs& a, float* red, floa
   const int grp = wave_id() / a.wpr;
   const int tg = (int)threadIdx.x - grp * G;
   const int n = a.n;
-  const int64_t start = (int64_t)blockIdx.x * a.rpb;
-  const int64_t end = start + a.rpb < a.rows ? start + a.rpb : a.rows;
-  const int iters = (int)((a.rpb + gpb - 1) / gpb);
+  const int64_t step = (int64_t)gridDim.x * gpb;  // grid-strided rows
+  const int64_t first = (int64_t)blockIdx.x * gpb + grp;
+  const int iters = (int)((a.rows + step - 1) / step);
   const bool want_dw = a.part != nullptr;
   const Span rw = make_span(a.w, (uint32_t)n * 4u);
   const float inv_n = 1.0f / (float)n;
@@ -411,8 +413,8 @@ __device__ __forceinline__ void bwd_rows_fast(const BwdArgs& a, float* red, floa
     for (int k = 0; k < NV; ++k) Chunk<float>::store(acc + 8 * (tg + k * G), zero);
   }
 
-  int64_t row = start + grp;
-  bool ok = row < end;
+  int64_t row = first;
+  bool ok = row < a.rows;
   Raw<TDY> rdy[NV];
   Raw<TX> rx[NV];
   {
@@ -427,8 +429,8 @@ __device__ __forceinline__ void bwd_rows_fast(const BwdArgs& a, float* red, floa
   float inv_next = (a.rstd != nullptr && ok) ? a.rstd[row] : 1.f;
 
   for (int it = 0; it < iters; ++it) {
-    const int64_t nrow = row + gpb;
-    const bool nok = it + 1 < iters && nrow < end;
+    const int64_t nrow = row + step;
+    const bool nok = it + 1 < iters && nrow < a.rows;
     // prefetch the next row (a row that does not exist reads nothing: 0-byte span)
     Raw<TDY> ndy[NV];
     Raw<TX> nx[NV];
