@@ -221,13 +221,17 @@ int esep_rmsnorm_bwd(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
   if (n_special > 0) vec = vec && aligned16(slot);
   a.vec = vec ? 1 : 0;
 
-  // LDS for the weight gradient. The fast kernel (vector rows, one dy, xhat from x, no dr_out)
-  // keeps one accumulator slot of nv * 64 * wpr * 8 floats per row group; the general kernel
-  // parks at most bwd_tree_lds of them at once (it always runs NV = 3 element-wise).
+  // LDS. The fast kernel (vector rows, one dy, xhat from x, no dr_out) stages the weight vector
+  // in one slot of nv * 64 * wpr * 8 floats and, with a weight gradient, keeps one accumulator
+  // slot per row group (at most (16 + 1) * 3 * 2 KiB per wpr: <= 144 KiB for n <= 16384). The
+  // general kernel parks at most bwd_tree_lds slots at once (it always runs NV = 3 element-wise).
   const bool fast = vec && n_dy == 1 && !from_y && dr_out == nullptr && n_special == 0;
+  const size_t slot_bytes = (size_t)nv * 64 * wpr * 8 * sizeof(float);
   size_t lds = 0;
-  if (dw)
-    lds = fast ? (size_t)gpb * nv * 64 * wpr * 8 * sizeof(float) : bwd_tree_lds(gpb, vec ? nv : 3, wpr);
+  if (fast)
+    lds = (dw ? (size_t)gpb + 1 : 1) * slot_bytes;
+  else if (dw)
+    lds = bwd_tree_lds(gpb, vec ? nv : 3, wpr);
   bool sup = false;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = esep::launch_rmsnorm_bwd(a, xdt, dydt, odt, nv, dim3((unsigned)blocks),

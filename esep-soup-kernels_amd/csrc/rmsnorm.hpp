@@ -388,10 +388,12 @@ __device__ __forceinline__ void bwd_rows(const BwdArgs& a, float* red, float* ld
 }
 
 // Fast backward for the common call: one gradient of y, xhat from x (not from y), no dr_out,
-// 16-byte-aligned whole chunks. The next row's dy and x are prefetched raw (still packed)
-// while the current row is computed, so each wavefront keeps two rows of loads in flight.
-// The weight-gradient accumulators live in LDS (one slot of NV * G * 8 floats per row group,
-// indexed by column) instead of registers; at the end the block sums the slots in group order.
+// 16-byte-aligned whole chunks. LDS holds, per block, the weight vector (staged once, read by
+// every row instead of through L2: at n = 3584 that is 14 KiB per row) and, with a weight
+// gradient, one fp32 accumulator slot of NV * G * 8 floats per row group, indexed by column; at
+// the end the block sums the slots in group order. Each row's dy and x are loaded at the top of
+// its iteration: prefetching the next row into registers measured slower than the occupancy it
+// costs (the plain loop needs about 80 VGPRs at NV = 3, so 5 wavefronts per SIMD fit).
 template <int NV, typename TX, typename TDY, typename TO>
 __device__ __forceinline__ void bwd_rows_fast(const BwdArgs& a, float* red, float* lds) {
   const int G = kWave * a.wpr;
@@ -403,48 +405,37 @@ __device__ __forceinline__ void bwd_rows_fast(const BwdArgs& a, float* red, floa
   const int64_t first = (int64_t)blockIdx.x * gpb + grp;
   const int iters = (int)((a.rows + step - 1) / step);
   const bool want_dw = a.part != nullptr;
-  const Span rw = make_span(a.w, (uint32_t)n * 4u);
   const float inv_n = 1.0f / (float)n;
-  const int stride = NV * G * 8;
+  const int stride = NV * G * 8;  // floats per slot (>= n; the tail past n stays 0)
   float* acc = lds + grp * stride;
+  float* wl = lds + (want_dw ? gpb * stride : 0);
+  for (int q = threadIdx.x; q < stride / 4; q += blockDim.x) {
+    f32x4 t = {0.f, 0.f, 0.f, 0.f};
+    if (4 * q < n) t = *reinterpret_cast<const f32x4*>(a.w + 4 * q);
+    *reinterpret_cast<f32x4*>(wl + 4 * q) = t;
+  }
   if (want_dw) {
     const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int k = 0; k < NV; ++k) Chunk<float>::store(acc + 8 * (tg + k * G), zero);
   }
-
-  int64_t row = first;
-  bool ok = row < a.rows;
-  Raw<TDY> rdy[NV];
-  Raw<TX> rx[NV];
-  {
-    const Span sd = row_rsrc<TDY>(a.dy[0], row, a.ld_dy, n, ok);
-    const Span sx = row_rsrc<TX>(a.x, row, a.ld_x, n, ok);
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      rdy[k] = Buf<TDY>::template load_raw<kStream>(sd, (tg + k * G) * 8 * sizeof(TDY));
-      rx[k] = Buf<TX>::template load_raw<kStream>(sx, (tg + k * G) * 8 * sizeof(TX));
-    }
-  }
-  float inv_next = (a.rstd != nullptr && ok) ? a.rstd[row] : 1.f;
+  __syncthreads();
 
   for (int it = 0; it < iters; ++it) {
-    const int64_t nrow = row + step;
-    const bool nok = it + 1 < iters && nrow < a.rows;
-    // prefetch the next row (a row that does not exist reads nothing: 0-byte span)
-    Raw<TDY> ndy[NV];
-    Raw<TX> nx[NV];
+    const int64_t row = first + (int64_t)it * step;
+    const bool ok = row < a.rows;  // a row that does not exist reads 0 and writes nothing
+    Raw<TDY> rdy[NV];
+    Raw<TX> rx[NV];
     {
-      const Span sd = row_rsrc<TDY>(a.dy[0], nrow, a.ld_dy, n, nok);
-      const Span sx = row_rsrc<TX>(a.x, nrow, a.ld_x, n, nok);
+      const Span sd = row_rsrc<TDY>(a.dy[0], row, a.ld_dy, n, ok);
+      const Span sx = row_rsrc<TX>(a.x, row, a.ld_x, n, ok);
 #pragma unroll
       for (int k = 0; k < NV; ++k) {
-        ndy[k] = Buf<TDY>::template load_raw<kStream>(sd, (tg + k * G) * 8 * sizeof(TDY));
-        nx[k] = Buf<TX>::template load_raw<kStream>(sx, (tg + k * G) * 8 * sizeof(TX));
+        rdy[k] = Buf<TDY>::template load_raw<kStream>(sd, (tg + k * G) * 8 * sizeof(TDY));
+        rx[k] = Buf<TX>::template load_raw<kStream>(sx, (tg + k * G) * 8 * sizeof(TX));
       }
     }
-    float inv = inv_next;
-    inv_next = (a.rstd != nullptr && nok) ? a.rstd[nrow] : 1.f;
+    float inv = (a.rstd != nullptr && ok) ? a.rstd[row] : 1.f;
 
     float dy[NV][8], x[NV][8];
 #pragma unroll
@@ -478,7 +469,7 @@ __device__ __forceinline__ void bwd_rows_fast(const BwdArgs& a, float* red, floa
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
       float w8[8];
-      bload<true, float, kCached>(rw, (tg + k * G) * 32, w8);
+      Chunk<float>::load(wl + 8 * (tg + k * G), w8);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         dy[k][e] *= w8[e];
@@ -500,13 +491,6 @@ __device__ __forceinline__ void bwd_rows_fast(const BwdArgs& a, float* red, floa
 #pragma unroll
       for (int k = 0; k < NV; ++k) bstore<true, TO>(so, (tg + k * G) * 8 * sizeof(TO), dy[k]);
     }
-#pragma unroll
-    for (int k = 0; k < NV; ++k) {
-      rdy[k] = ndy[k];
-      rx[k] = nx[k];
-    }
-    row = nrow;
-    ok = nok;
   }
   if (want_dw) {
     // block sum: column quads over all threads, groups added in group order
