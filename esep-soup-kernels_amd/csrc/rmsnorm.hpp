@@ -390,10 +390,11 @@ __device__ __forceinline__ void bwd_rows(const BwdArgs& a, float* red, float* ld
 // Fast backward for the common call: one gradient of y, xhat from x (not from y), no dr_out,
 // 16-byte-aligned whole chunks. LDS holds, per block, the weight vector (staged once, read by
 // every row instead of through L2: at n = 3584 that is 14 KiB per row) and, with a weight
-// gradient, one fp32 accumulator slot of NV * G * 8 floats per row group, indexed by column; at
-// the end the block sums the slots in group order. Each row's dy and x are loaded at the top of
-// its iteration: prefetching the next row into registers measured slower than the occupancy it
-// costs (the plain loop needs about 80 VGPRs at NV = 3, so 5 wavefronts per SIMD fit).
+// gradient, one slot of NV * G * 8 floats per row group, indexed by column. Each lane keeps its
+// dy * xhat sums in registers over the rows of its group (the LDS of a weight-gradient block
+// already limits a CU to that one block, so the registers cost no occupancy), parks them in its
+// group's slot at the end, and the block sums the slots in group order. Each row's dy and x are
+// loaded at the top of its iteration: prefetching the next row into registers measured slower.
 template <int NV, typename TX, typename TDY, typename TO>
 __device__ __forceinline__ void bwd_rows_fast(const BwdArgs& a, float* red, float* lds) {
   const int G = kWave * a.wpr;
@@ -414,11 +415,11 @@ __device__ __forceinline__ void bwd_rows_fast(const BwdArgs& a, float* red, floa
     if (4 * q < n) t = *reinterpret_cast<const f32x4*>(a.w + 4 * q);
     *reinterpret_cast<f32x4*>(wl + 4 * q) = t;
   }
-  if (want_dw) {
-    const float zero[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  float dwa[NV][8];
 #pragma unroll
-    for (int k = 0; k < NV; ++k) Chunk<float>::store(acc + 8 * (tg + k * G), zero);
-  }
+  for (int k = 0; k < NV; ++k)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dwa[k][e] = 0.f;
   __syncthreads();
 
   for (int it = 0; it < iters; ++it) {
@@ -455,16 +456,11 @@ __device__ __forceinline__ void bwd_rows_fast(const BwdArgs& a, float* red, floa
     for (int k = 0; k < NV; ++k)
 #pragma unroll
       for (int e = 0; e < 8; ++e) x[k][e] *= inv;
-    if (want_dw && ok) {
+    // (a row that does not exist has dy = x = 0 and adds nothing)
 #pragma unroll
-      for (int k = 0; k < NV; ++k) {
-        float t[8];
-        Chunk<float>::load(acc + 8 * (tg + k * G), t);
+    for (int k = 0; k < NV; ++k)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) t[e] = fmaf(dy[k][e], x[k][e], t[e]);
-        Chunk<float>::store(acc + 8 * (tg + k * G), t);
-      }
-    }
+      for (int e = 0; e < 8; ++e) dwa[k][e] = fmaf(dy[k][e], x[k][e], dwa[k][e]);
     float p = 0.f;
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
@@ -493,6 +489,8 @@ __device__ __forceinline__ void bwd_rows_fast(const BwdArgs& a, float* red, floa
     }
   }
   if (want_dw) {
+#pragma unroll
+    for (int k = 0; k < NV; ++k) Chunk<float>::store(acc + 8 * (tg + k * G), dwa[k]);
     // block sum: column quads over all threads, groups added in group order
     __syncthreads();
     float* dst = a.part + (int64_t)blockIdx.x * n;
