@@ -273,6 +273,63 @@ def time_graph(g, reps):
     return e0.elapsed_time(e1) / reps, (t1 - t0) * 1e3 / reps
 
 
+def api_bytes(T, H, k_dy, fwd):
+    """The reference API's pattern (AddRMSNorm in the packed decoder): fp32 residual r, bf16
+    delta / y / dys, fp32 r_out / dr_out / dr, bf16 ddelta, rstd saved, frozen weight (no dw)."""
+    if fwd:  # r_in, delta -> r_out, y, rstd
+        return T * H * (4 + 2 + 4 + 2) + 4 * T
+    # k dys, x (= r_out), dr_out -> dr, ddelta; rstd read
+    return T * H * (2 * k_dy + 4 + 4 + 4 + 2) + 4 * T
+
+
+def run_api_variant(dev, reps, n_sets=6):
+    """Times the reference API's own calls at the config-4 shape (T = 8192, H = 1536): the
+    add_rmsnorm forward, and the backward of the input norm (3 consumers) and of the
+    post-attention norm (2 consumers), each in a graph over n_sets distinct tensor sets."""
+    import torch
+
+    from solution.body import _hip
+
+    T, H, eps = CFG4["B"] * CFG4["S"], CFG4["H"], CFG4["eps"]
+    g = torch.Generator(device=dev).manual_seed(7)
+    bf = torch.bfloat16
+
+    def rn(dt, *shape):
+        return torch.randn(shape, generator=g, device=dev, dtype=torch.float32).to(dt)
+
+    sets = []
+    for _ in range(n_sets):
+        sets.append(dict(r=rn(torch.float32, T, H), d=rn(bf, T, H), ro=torch.empty(T, H, device=dev),
+                         y=torch.empty(T, H, device=dev, dtype=bf), rstd=torch.rand(T, device=dev) + 0.5,
+                         w=1 + 0.02 * torch.randn(H, generator=g, device=dev),
+                         dys=[rn(bf, T, H) for _ in range(3)], dro=rn(torch.float32, T, H),
+                         dr=torch.empty(T, H, device=dev), dd=torch.empty(T, H, device=dev, dtype=bf)))
+    calls = {
+        "add_rmsnorm_fwd": (lambda: [_hip.rmsnorm_fwd(s["r"], s["w"], s["y"], eps, delta=s["d"], r_out=s["ro"],
+                                                      rstd=s["rstd"]) for s in sets], api_bytes(T, H, 0, True)),
+        "add_rmsnorm_bwd_3dy": (lambda: [_hip.rmsnorm_bwd(s["dys"], s["r"], s["w"], eps, rstd=s["rstd"],
+                                                          dr_out=s["dro"], dr=s["dr"], dx=s["dd"]) for s in sets],
+                                api_bytes(T, H, 3, False)),
+        "add_rmsnorm_bwd_2dy": (lambda: [_hip.rmsnorm_bwd(s["dys"][:2], s["r"], s["w"], eps, rstd=s["rstd"],
+                                                          dr_out=s["dro"], dr=s["dr"], dx=s["dd"]) for s in sets],
+                                api_bytes(T, H, 2, False)),
+    }
+    out = {}
+    for name, (fn, nbytes) in calls.items():
+        kg = capture(fn)
+        time_graph(kg, 2)
+        ms, _ = time_graph(kg, reps)
+        us = ms * 1e3 / n_sets
+        out[name] = {"us": round(us, 2), "GB/s": round(nbytes / (us * 1e-6) / 1e9, 1), "bytes": nbytes}
+        log(f"api {name}: {us:.2f} us/launch, {nbytes / (us * 1e-6) / 1e9:.0f} GB/s")
+    del sets
+    torch.cuda.empty_cache()
+    return {"workload": "the reference API's calls at T=8192, H=1536: add_rmsnorm forward (fp32 r_in + "
+                        "bf16 delta -> fp32 r_out, bf16 y, rstd) and AddRMSNorm backward with 3 or 2 "
+                        "bf16 dys and fp32 dr_out -> fp32 dr + bf16 ddelta (frozen weight, rstd saved)",
+            "kernels": out}
+
+
 def kernel_rooflines(body, reps):
     """Per-launch time of each entry point: a graph of one launch per layer of that kernel
     alone (distinct tensors, as in the sweep), replayed `reps` times, timed with HIP events
@@ -423,6 +480,7 @@ def main():
     del body
     torch.cuda.empty_cache()
     c5 = None if args.no_config5 else run_config5(dev, max(args.steps // 3, 5))
+    api = run_api_variant(dev, max(args.steps // 3, 5))
 
     cpu = None
     if not args.no_cpu:
@@ -449,6 +507,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "config5": c5,
+        "api_variant": api,
     }
     print(json.dumps(out), flush=True)
     return 0

@@ -165,9 +165,9 @@ int esep_rmsnorm_bwd(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
   if (n_special < 0 || (n_special > 0 && (!from_y || slot == nullptr || xs == nullptr)))
     return fail(ESEP_EINVAL, "rmsnorm_bwd: n_special > 0 needs from_y, slot and xs");
   if (dx_lp != nullptr && !float_dt(dx_dt)) return fail(ESEP_EINVAL, "rmsnorm_bwd: dx dtype");
-  if (dw != nullptr) {
-    if (!float_dt(dw_dt) || dw_partials == nullptr)
-      return fail(ESEP_EINVAL, "rmsnorm_bwd: dw needs dw_partials and a float dtype");
+  if (dw != nullptr && (!float_dt(dw_dt) || dw_partials == nullptr))
+    return fail(ESEP_EINVAL, "rmsnorm_bwd: dw needs dw_partials and a float dtype");
+  if (dw_partials != nullptr) {
     const int64_t want = esep_rmsnorm_partials(rows, n);
     if (rows > 0 && n_partials != want)
       return fail(ESEP_ESHAPE, "rmsnorm_bwd: n_partials=%lld, this shape needs %lld",
@@ -176,7 +176,16 @@ int esep_rmsnorm_bwd(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
   if ((n_dy > 0 && (ld_dy < n || ld_x < n)) ||
       ((dr_out || dr_f32 || dx_lp) && ld_out < n))
     return fail(ESEP_ESHAPE, "rmsnorm_bwd: leading dimension smaller than n");
-  if (rows == 0) return 0;
+  if (rows == 0) {  // no rows: dw is the empty sum, 0
+    if (dw == nullptr) return 0;
+    bool sup = false;
+    const hipError_t e = esep::launch_dgamma_reduce(dw_partials, 0, (int)n, dw, dw_dt,
+                                                    static_cast<hipStream_t>(stream), &sup);
+    return e == hipSuccess ? 0 : hip_fail(e, "rmsnorm_bwd dw reduce launch");
+  }
+  // Stage 1 (weight-gradient partials) runs when a workspace is given: with dw, stage 2
+  // follows here; without, the caller reduces later (esep_dgamma_reduce).
+  const bool part = dw_partials != nullptr;
 
   esep::BwdArgs a{};
   for (int i = 0; i < n_dy; ++i) a.dy[i] = dys[i];
@@ -194,7 +203,7 @@ int esep_rmsnorm_bwd(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
   a.dr = dr_f32;
   a.dx = dx_lp;
   a.ld_out = ld_out;
-  a.part = dw ? dw_partials : nullptr;
+  a.part = part ? dw_partials : nullptr;
   a.rows = rows;
   a.n = (int)n;
   a.eps = eps;
@@ -203,8 +212,8 @@ int esep_rmsnorm_bwd(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
   a.wpr = wpr;
   // Without a weight gradient every row group owns one row and small blocks (4 row groups of
   // one wavefront, or one group of wpr wavefronts) let finished waves be replaced one by one.
-  const int gpb = dw ? bwd_groups(wpr) : (wpr >= 4 ? 1 : 4 / wpr);
-  const int64_t blocks = dw ? bwd_partials(rows, n) : (rows + gpb - 1) / gpb;
+  const int gpb = part ? bwd_groups(wpr) : (wpr >= 4 ? 1 : 4 / wpr);
+  const int64_t blocks = part ? bwd_partials(rows, n) : (rows + gpb - 1) / gpb;
   if (blocks > 0x7fffffff) return fail(ESEP_ESHAPE, "rmsnorm_bwd: too many rows");
 
   const int xdt = n_dy > 0 ? x_dt : ESEP_F32;
@@ -229,8 +238,8 @@ int esep_rmsnorm_bwd(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
   const size_t slot_bytes = (size_t)nv * 64 * wpr * 8 * sizeof(float);
   size_t lds = 0;
   if (fast)
-    lds = (dw ? (size_t)gpb + 1 : 1) * slot_bytes;
-  else if (dw)
+    lds = (part ? (size_t)gpb + 1 : 1) * slot_bytes;
+  else if (part)
     lds = bwd_tree_lds(gpb, vec ? nv : 3, wpr);
   bool sup = false;
   hipStream_t s = static_cast<hipStream_t>(stream);
@@ -244,6 +253,20 @@ int esep_rmsnorm_bwd(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
     if (e != hipSuccess) return hip_fail(e, "rmsnorm_bwd dw reduce launch");
   }
   return 0;
+}
+
+int esep_dgamma_reduce(const float* partials, int64_t n_partials, int64_t n, void* dw, int dw_dt,
+                       void* stream) {
+  g_err[0] = 0;
+  if (n < 1 || n > ESEP_NORM_MAX_COLS)
+    return fail(ESEP_ESHAPE, "dgamma_reduce: n=%lld outside [1, %d]", (long long)n, ESEP_NORM_MAX_COLS);
+  if (n_partials < 0) return fail(ESEP_ESHAPE, "dgamma_reduce: n_partials < 0");
+  if (dw == nullptr || !float_dt(dw_dt) || (n_partials > 0 && partials == nullptr))
+    return fail(ESEP_EINVAL, "dgamma_reduce: dw, its float dtype and the partials are required");
+  bool sup = false;
+  const hipError_t e = esep::launch_dgamma_reduce(partials, n_partials, (int)n, dw, dw_dt,
+                                                  static_cast<hipStream_t>(stream), &sup);
+  return e == hipSuccess ? 0 : hip_fail(e, "dgamma_reduce launch");
 }
 
 int esep_rope(const void* q, const int64_t q_strides[3], const void* q_delta,

@@ -41,6 +41,7 @@ SIGNATURES = {
     "esep_rmsnorm_bwd": (_i32, [_vp, _i32, _i32, _i64, _vp, _vp, _i32, _i64, _i32, _vp, _vp, _vp,
                                 _vp, _i32, _vp, _vp, _i32, _i64, _vp, _i64, _vp, _i32, _i64, _i64,
                                 _f32, _vp]),
+    "esep_dgamma_reduce": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp]),
     "esep_rope": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64,
                          _i32, _i32, _i32, _vp, _i32, _vp, _vp, _i32, _vp, _f32, _vp]),
 }
@@ -171,11 +172,13 @@ def rmsnorm_partials(rows, n):
 
 
 def rmsnorm_bwd(dys, x, w, eps, from_y=False, rstd=None, dr_out=None, slot=None, xs=None,
-                n_special=0, dr=None, dx=None, dw=None, workspace=None, name="_add_rmsnorm_bwd"):
+                n_special=0, dr=None, dx=None, dw=None, workspace=None, partials=None,
+                name="_add_rmsnorm_bwd"):
     """Backward of rmsnorm_fwd; see esep_rmsnorm_bwd. dys: list of [rows, n] tensors of one
     dtype (their sum is dy). dr: fp32 [rows, n] out; dx: low-precision [rows, n] out;
     dw: [n] out, reduced through a [P, n] fp32 workspace (P = rmsnorm_partials(rows, n));
-    pass `workspace` to reuse one, else it is allocated here."""
+    pass `workspace` to reuse one, else it is allocated here. Without dw, `partials` (an fp32
+    [P, n] tensor) receives the weight-gradient partials for a later dgamma_reduce."""
     rows, n = x.shape
     dev = _dev(x, w, rstd, dr_out, slot, xs, dr, dx, dw, *dys)
     if len(dys) > 5:
@@ -195,7 +198,15 @@ def rmsnorm_bwd(dys, x, w, eps, from_y=False, rstd=None, dr_out=None, slot=None,
     ld_out = louts.pop() if louts else n
     part = None
     n_part = 0
-    if dw is not None:
+    if dw is not None and partials is not None:
+        raise EsepError("pass either dw (reduced here) or partials (reduced later), not both")
+    if partials is not None:
+        n_part = rmsnorm_partials(rows, n)
+        if (partials.dtype != torch.float32 or not partials.is_contiguous()
+                or tuple(partials.shape) != (n_part, n) or partials.device != dev):
+            raise EsepError(f"partials must be a contiguous fp32 [{n_part}, {n}] tensor")
+        part = partials
+    elif dw is not None:
         n_part = rmsnorm_partials(rows, n)
         if workspace is not None:
             if (workspace.dtype != torch.float32 or not workspace.is_contiguous()
@@ -214,6 +225,20 @@ def rmsnorm_bwd(dys, x, w, eps, from_y=False, rstd=None, dr_out=None, slot=None,
         rows, n, float(eps), _stream(dev))
     _check(rc, "esep_rmsnorm_bwd")
     _record(name)
+
+
+def dgamma_reduce(partials, dw):
+    """dw[j] = sum_p partials[p, j] (fp32 [P, n] contiguous) in the fixed order of
+    esep_dgamma_reduce; dw: [n] fp32 / fp16 / bf16 out."""
+    dev = _dev(partials, dw)
+    if partials.dtype != torch.float32 or not partials.is_contiguous() or partials.dim() != 2:
+        raise EsepError("partials must be a contiguous fp32 [P, n] tensor")
+    P, n = partials.shape
+    if not dw.is_contiguous() or dw.numel() != n:
+        raise EsepError(f"dw must be a contiguous [{n}] tensor")
+    rc = lib().esep_dgamma_reduce(_p(partials) if P else None, P, n, _p(dw), dtype_code(dw.dtype),
+                                  _stream(dev))
+    _check(rc, "esep_dgamma_reduce")
 
 
 def rope(q, k, qo, ko, inv_freq, sign, q_delta=None, positions=None, cu_seqlens=None,

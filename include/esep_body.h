@@ -109,9 +109,10 @@ int64_t esep_rmsnorm_partials(int64_t rows, int64_t n);
  *   dr     = rstd * (g - xhat * proj) (+ dr_out)         (dr_out fp32 [rows, n] or NULL)
  *   dr_f32 [rows, n] fp32 or NULL  <- dr
  *   dx_lp  [rows, n] dx_dt or NULL <- dr rounded to dx_dt
- *   dw_j   = sum_t dy_tj * xhat_tj             when dw != NULL: stage 1 writes the
- *            partials [P, n] fp32 (P = esep_rmsnorm_partials(rows, n), n_partials must equal P),
- *            stage 2 sums them in a fixed order into dw [n] (dw_dt)
+ *   dw_j   = sum_t dy_tj * xhat_tj             when dw_partials != NULL: stage 1 writes the
+ *            partials [P, n] fp32 (P = esep_rmsnorm_partials(rows, n), n_partials must equal P);
+ *            with dw != NULL stage 2 then sums them in a fixed order into dw [n] (dw_dt), else
+ *            the caller reduces them later with esep_dgamma_reduce. rows == 0 gives dw = 0.
  * n_dy == 0 and dr_out != NULL gives dr = dr_out. Contiguous rows for dr_out, dr_f32, dx_lp
  * use ld_out; x uses ld_x.
  */
@@ -124,6 +125,17 @@ int esep_rmsnorm_bwd(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
                      float* dr_f32, void* dx_lp, int dx_dt, int64_t ld_out,
                      float* dw_partials, int64_t n_partials, void* dw, int dw_dt,
                      int64_t rows, int64_t n, float eps, void* stream);
+
+/*
+ * Stage 2 of the weight gradient on its own: dw[j] = sum_{p < n_partials} partials[p, j], summed
+ * in an order that depends on n_partials only (bitwise equal to the stage 2 inside
+ * esep_rmsnorm_bwd for the same partials). partials: fp32 [n_partials, n] contiguous;
+ * n_partials == 0 writes zeros. No reference counterpart (the reference computes no weight
+ * gradient: norm_rope.py:286 returns None for it); for callers that run stage 1 per micro-batch
+ * or on several streams and reduce once.
+ */
+int esep_dgamma_reduce(const float* partials, int64_t n_partials, int64_t n, void* dw, int dw_dt,
+                       void* stream);
 
 /*
  * Rotary embedding on q and k in one launch (forward with sin_sign = +1, backward with -1).

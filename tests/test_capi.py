@@ -73,7 +73,19 @@ def test_rmsnorm_bwd_validation():
     assert bwd(from_y=1) == -1 and b"rstd" in lib.esep_last_error()
     assert bwd(dw=1) == -1  # no partials workspace
     assert bwd(dw=1, part=1, n_part=3) == -2 and b"needs 1" in lib.esep_last_error()
+    assert bwd(part=1, n_part=3) == -2  # partials only: the count is checked too
+    assert bwd(dw=1, dw_dt=3, part=1, n_part=1) == -1  # int32 dw
     assert bwd(rows=0) == 0
+
+
+def test_dgamma_reduce_validation():
+    lib = _hip.lib()
+    assert lib.esep_dgamma_reduce(1, 4, 0, 1, 0, None) == -2
+    assert lib.esep_dgamma_reduce(1, 4, 16385, 1, 0, None) == -2
+    assert lib.esep_dgamma_reduce(1, -1, 8, 1, 0, None) == -2
+    assert lib.esep_dgamma_reduce(1, 4, 8, None, 0, None) == -1
+    assert lib.esep_dgamma_reduce(None, 4, 8, 1, 0, None) == -1
+    assert lib.esep_dgamma_reduce(1, 4, 8, 1, 3, None) == -1 and b"dgamma" in lib.esep_last_error()
 
 
 def test_rope_validation():

@@ -5,6 +5,7 @@ oracle (oracle/norm_rope_ref.py) on seeded inputs.
 Tolerances: 16-bit outputs atol 2e-3 / rtol 1e-2 against the fp64 oracle (the north-star
 bar), fp32 outputs 1e-5; the reference's own tests keep their own tolerances (quoted)."""
 
+import ctypes
 import numpy as np
 import pytest
 import torch
@@ -395,6 +396,40 @@ def test_dgamma_deterministic(T):
     assert torch.equal(runs[0], dw2)
     _, dw64 = ref.rmsnorm_bwd(np64(dy), np64(x), np64(w), EPS)
     assert_close(np64(runs[0]), dw64, 1e-5 * np.abs(dw64).max(), 1e-5, "dw")
+
+
+@pytest.mark.parametrize("T,n", [(1, 1536), (4097, 1536), (300, 3584), (65, 1001)])
+def test_dgamma_partials_then_reduce(T, n):
+    """Stage 1 alone (partials into the caller's buffer) and esep_dgamma_reduce later give the
+    fused call's dw bit for bit, with dx unchanged; no rows and no partials give dw = 0."""
+    from solution.body import _hip
+
+    g = gen(T + n)
+    x = randn((T, n), g, dtype=torch.bfloat16)
+    dy = randn((T, n), g, dtype=torch.bfloat16)
+    w = (1 + 0.02 * torch.randn(n, generator=g)).to(DEV)
+    dx1, dx2 = torch.empty_like(x), torch.empty_like(x)
+    dw1, dw2 = torch.empty(n, device=DEV), torch.full((n,), float("nan"), device=DEV)
+    _hip.rmsnorm_bwd([dy], x, w, EPS, dx=dx1, dw=dw1)
+    part = torch.full((_hip.rmsnorm_partials(T, n), n), float("nan"), device=DEV)
+    _hip.rmsnorm_bwd([dy], x, w, EPS, dx=dx2, partials=part)
+    _hip.dgamma_reduce(part, dw2)
+    assert torch.equal(dx1, dx2) and torch.equal(dw1, dw2)
+    _, dw64 = ref.rmsnorm_bwd(np64(dy), np64(x), np64(w), EPS)
+    assert_close(np64(dw2), dw64, 1e-4 * np.abs(dw64).max(), 1e-4, "dw")
+    # rows = 0 through the C ABI (torch gives empty views a NULL data pointer, which the ABI
+    # rejects even for empty inputs, so the full tensors' pointers stand in)
+    z = torch.full((n,), float("nan"), device=DEV, dtype=torch.bfloat16)
+    lib = _hip.lib()
+    rc = lib.esep_rmsnorm_bwd((ctypes.c_void_p * 5)(dy.data_ptr()), 1, 2, n, None, x.data_ptr(),
+                              2, n, 0, None, w.data_ptr(), None, None, 0, None, dx1.data_ptr(), 2,
+                              n, part.data_ptr(), 0, z.data_ptr(), 2, 0, n, EPS,
+                              torch.cuda.current_stream().cuda_stream)
+    assert rc == 0, lib.esep_last_error()
+    assert torch.equal(z, torch.zeros_like(z))
+    z.fill_(float("nan"))
+    _hip.dgamma_reduce(torch.empty((0, n), device=DEV), z)
+    assert torch.equal(z, torch.zeros_like(z))
 
 
 def test_add_rmsnorm_weight_grad():
