@@ -1,0 +1,209 @@
+// Varlen causal attention forward (see attention.hpp for the layout and the MFMA mapping).
+#include <cmath>
+
+#include "attention.hpp"
+
+namespace esep {
+namespace {
+
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <typename T>
+struct Mfma;
+template <>
+struct Mfma<__bf16> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x16 run(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma<_Float16> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x16 run(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <typename V>
+__device__ __forceinline__ V ld16(const void* p) {
+  return __builtin_bit_cast(V, *reinterpret_cast<const uint4*>(p));
+}
+
+// 8 elements from two 4-element (8-byte) halves.
+template <typename V>
+__device__ __forceinline__ V ld8x2(const void* lo, const void* hi) {
+  const uint2 a = *reinterpret_cast<const uint2*>(lo);
+  const uint2 b = *reinterpret_cast<const uint2*>(hi);
+  return __builtin_bit_cast(V, make_uint4(a.x, a.y, b.x, b.y));
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(kAttnThreads) void k_attn_fwd(const AttnArgs a) {
+  using V8 = typename Mfma<T>::v8;
+  constexpr int BN = kAttnBN;
+  constexpr int KP = D + 8;   // K row pitch in LDS (elements): rows land on different banks
+  constexpr int VP = BN + 8;  // V^T row pitch in LDS (elements)
+  __shared__ __align__(16) T ks[BN * KP];
+  __shared__ __align__(16) T vt[D * VP];
+
+  const int seq = blockIdx.z, h = blockIdx.y;
+  // sequence bounds, clamped into [0, T] so that malformed offsets stay in bounds
+  const int tt = (int)a.T;
+  const int c0 = a.cu[seq], c1 = a.cu[seq + 1];
+  const int start = c0 < 0 ? 0 : (c0 > tt ? tt : c0);
+  const int end = c1 < start ? start : (c1 > tt ? tt : c1);
+  const int ntiles = (end - start + kAttnBM - 1) / kAttnBM;
+  if ((int)blockIdx.x >= ntiles) return;
+  const int q0 = start + (ntiles - 1 - (int)blockIdx.x) * kAttnBM;  // heaviest tiles first
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int lq = lane & 31, hi = lane >> 5;
+  const int kvh = h / (a.HQ / a.HK);
+  const int qw0 = q0 + 32 * w;                  // this wavefront's first query
+  const int qi = qw0 + lq;                      // this lane's query
+  const bool wave_live = qw0 < end;
+  const int wq_last = qw0 + 31 < end ? qw0 + 31 : end - 1;
+
+  // Q^T as the B operand: lane (lq, hi) holds Q[qi][16c + 8hi .. 16c + 8hi + 7] for chunk c.
+  V8 qb[D / 16];
+  {
+    const T* qrow = static_cast<const T*>(a.q) + (int64_t)qi * a.q_rs + (int64_t)h * D + 8 * hi;
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c)
+      qb[c] = qi < end ? ld16<V8>(qrow + 16 * c) : V8{};
+  }
+
+  f32x16 oacc[D / 32];
+#pragma unroll
+  for (int md = 0; md < D / 32; ++md) oacc[md] = f32x16{};
+  float m = -INFINITY, l = 0.f;
+  const int kend = end < q0 + kAttnBM ? end : q0 + kAttnBM;
+  const T* kbase = static_cast<const T*>(a.k) + (int64_t)kvh * D;
+  const T* vbase = static_cast<const T*>(a.v) + (int64_t)kvh * D;
+
+  for (int kt = start; kt < kend; kt += BN) {
+    __syncthreads();  // the previous tile's LDS reads are done
+    // K tile, row-major: 64 keys x D/8 chunks of 16 bytes (keys past kend read as 0).
+    for (int idx = tid; idx < BN * (D / 8); idx += kAttnThreads) {
+      const int key = idx % BN, dc = idx / BN;
+      uint4 val = make_uint4(0, 0, 0, 0);
+      if (kt + key < kend)
+        val = *reinterpret_cast<const uint4*>(kbase + (int64_t)(kt + key) * a.k_rs + 8 * dc);
+      *reinterpret_cast<uint4*>(&ks[key * KP + 8 * dc]) = val;
+    }
+    // V^T tile: a thread takes keys (2p, 2p + 1) of one 8-column chunk and writes 8 dwords
+    // (one per column d), each holding the two keys' values.
+    for (int idx = tid; idx < (BN / 2) * (D / 8); idx += kAttnThreads) {
+      const int p = idx % (BN / 2), dc = idx / (BN / 2);
+      const int kj = kt + 2 * p;
+      uint4 v0 = make_uint4(0, 0, 0, 0), v1 = make_uint4(0, 0, 0, 0);
+      if (kj < kend) v0 = *reinterpret_cast<const uint4*>(vbase + (int64_t)kj * a.v_rs + 8 * dc);
+      if (kj + 1 < kend) v1 = *reinterpret_cast<const uint4*>(vbase + (int64_t)(kj + 1) * a.v_rs + 8 * dc);
+      const uint32_t w0[4] = {v0.x, v0.y, v0.z, v0.w}, w1[4] = {v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t lo = (w0[e / 2] >> (16 * (e % 2))) & 0xffffu;
+        const uint32_t up = (w1[e / 2] >> (16 * (e % 2))) & 0xffffu;
+        *reinterpret_cast<uint32_t*>(&vt[(8 * dc + e) * VP + 2 * p]) = lo | (up << 16);
+      }
+    }
+    __syncthreads();
+    if (!wave_live || kt > wq_last) continue;  // every key of the tile is after this wave's queries
+
+    // S^T = K Q^T for the two 32-key halves of the tile; lane (lq, hi) gets the scores of query
+    // qi against keys kt + 32 sb + 8 (i / 4) + 4 hi + i % 4, i < 16.
+    float sc[2][16];
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      f32x16 acc = f32x16{};
+      const T* krow = &ks[(32 * sb + lq) * KP + 8 * hi];
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) acc = Mfma<T>::run(ld16<V8>(krow + 16 * c), qb[c], acc);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int kj = kt + 32 * sb + 8 * (i / 4) + 4 * hi + (i % 4);
+        sc[sb][i] = kj <= qi ? acc[i] * a.scale_log2 : -INFINITY;
+      }
+    }
+    // online softmax (base 2): running max m and sum l per query
+    float mx = -INFINITY;
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sc[sb][i]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float mnew = fmaxf(m, mx);
+    const float mu = mnew == -INFINITY ? 0.f : mnew;
+    const float alpha = exp2f(m - mu);
+    float ps = 0.f;
+    V8 pb[2][2];
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const float p = exp2f(sc[sb][i] - mu);
+        ps += p;
+        pb[sb][i / 8][i % 8] = (T)p;
+      }
+    ps += __shfl_xor(ps, 32);
+    l = l * alpha + ps;
+    m = mnew;
+    // O^T += V^T P^T over the 64 keys, contraction in the permuted key order of pb: element e
+    // of chunk (sb, c2) is key 32 sb + 16 c2 + 8 (e / 4) + 4 hi + e % 4.
+#pragma unroll
+    for (int md = 0; md < D / 32; ++md) {
+      oacc[md] *= alpha;
+      const T* vrow = &vt[(32 * md + lq) * VP + 4 * hi];
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2) {
+          const int kb = 32 * sb + 16 * c2;
+          oacc[md] = Mfma<T>::run(ld8x2<V8>(vrow + kb, vrow + kb + 8), pb[sb][c2], oacc[md]);
+        }
+    }
+  }
+
+  if (!wave_live || qi >= end) return;
+  // O = O^T / l: lane (lq, hi) holds columns d = 32 md + 8 j + 4 hi + (0..3) of query qi.
+  const float inv = l > 0.f ? 1.f / l : 0.f;
+  T* orow = static_cast<T*>(a.o) + (int64_t)qi * a.o_rs + (int64_t)h * D + 4 * hi;
+#pragma unroll
+  for (int md = 0; md < D / 32; ++md)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      T o4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o4[e] = (T)(oacc[md][4 * j + e] * inv);
+      *reinterpret_cast<uint2*>(orow + 32 * md + 8 * j) = __builtin_bit_cast(uint2, o4);
+    }
+  if (hi == 0 && a.lse != nullptr)
+    a.lse[(int64_t)h * a.T + qi] = (m + log2f(l)) * 0.69314718055994531f;
+}
+
+template <typename T>
+hipError_t fwd_d(const AttnArgs& a, int D, dim3 grid, hipStream_t s, bool* sup) {
+  *sup = true;
+  if (D == 128)
+    hipLaunchKernelGGL((k_attn_fwd<T, 128>), grid, dim3(kAttnThreads), 0, s, a);
+  else if (D == 64)
+    hipLaunchKernelGGL((k_attn_fwd<T, 64>), grid, dim3(kAttnThreads), 0, s, a);
+  else {
+    *sup = false;
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+}  // namespace
+
+hipError_t launch_attn_fwd(const AttnArgs& a, int dt, int D, int max_seqlen, hipStream_t s,
+                           bool* sup) {
+  const dim3 grid((max_seqlen + kAttnBM - 1) / kAttnBM, a.HQ, a.n_seq);
+  if (dt == 1) return fwd_d<_Float16>(a, D, grid, s, sup);
+  if (dt == 2) return fwd_d<__bf16>(a, D, grid, s, sup);
+  *sup = false;
+  return hipErrorInvalidValue;
+}
+
+}  // namespace esep

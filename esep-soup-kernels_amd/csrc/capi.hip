@@ -4,6 +4,7 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include "attention.hpp"
 #include "esep_body.h"
 #include "rmsnorm.hpp"
 #include "rope.hpp"
@@ -349,6 +350,51 @@ int esep_rope(const void* q, const int64_t q_strides[3], const void* q_delta,
   if (!sup) return fail(ESEP_EINVAL, "rope: unsupported dtype %d / D %d", dt, D);
   if (e != hipSuccess) return hip_fail(e, "rope launch");
   return 0;
+}
+
+int esep_attn_fwd(const void* q, int64_t q_rs, const void* k, int64_t k_rs, const void* v,
+                  int64_t v_rs, void* o, int64_t o_rs, float* lse, int dt, int64_t T, int HQ,
+                  int HK, int D, const int32_t* cu_seqlens, int n_seq, int max_seqlen,
+                  float scale, void* stream) {
+  g_err[0] = 0;
+  if (dt != ESEP_F16 && dt != ESEP_BF16)
+    return fail(ESEP_EINVAL, "attn_fwd: dtype %d is not fp16 / bf16", dt);
+  if (D != 64 && D != 128) return fail(ESEP_ESHAPE, "attn_fwd: D=%d not in {64, 128}", D);
+  if (T < 0 || T > 0x7fffffff || HQ < 1 || HK < 1 || HQ % HK != 0 || n_seq < 0 || max_seqlen < 0)
+    return fail(ESEP_ESHAPE, "attn_fwd: bad sizes T=%lld HQ=%d HK=%d n_seq=%d max_seqlen=%d",
+                (long long)T, HQ, HK, n_seq, max_seqlen);
+  if (q_rs < (int64_t)HQ * D || o_rs < (int64_t)HQ * D || k_rs < (int64_t)HK * D ||
+      v_rs < (int64_t)HK * D)
+    return fail(ESEP_ESHAPE, "attn_fwd: token stride smaller than heads * D");
+  if (T == 0 || n_seq == 0 || max_seqlen == 0) return 0;
+  if (q == nullptr || k == nullptr || v == nullptr || o == nullptr || cu_seqlens == nullptr)
+    return fail(ESEP_EINVAL, "attn_fwd: q, k, v, o and cu_seqlens are required");
+  if (!aligned16(q) || !aligned16(k) || !aligned16(v) || !aligned16(o) || (q_rs & 7) ||
+      (k_rs & 7) || (v_rs & 7) || (o_rs & 7))
+    return fail(ESEP_EALIGN, "attn_fwd: q, k, v, o need 16-byte alignment and token strides "
+                             "that are multiples of 8 elements");
+  if (!(scale > 0.f)) return fail(ESEP_EINVAL, "attn_fwd: scale must be positive");
+  esep::AttnArgs a{};
+  a.q = q;
+  a.k = k;
+  a.v = v;
+  a.o = o;
+  a.lse = lse;
+  a.cu = cu_seqlens;
+  a.q_rs = q_rs;
+  a.k_rs = k_rs;
+  a.v_rs = v_rs;
+  a.o_rs = o_rs;
+  a.T = T;
+  a.n_seq = n_seq;
+  a.HQ = HQ;
+  a.HK = HK;
+  a.scale = scale;
+  a.scale_log2 = scale * 1.4426950408889634f;
+  bool sup = false;
+  const hipError_t e = esep::launch_attn_fwd(a, dt, D, max_seqlen, static_cast<hipStream_t>(stream), &sup);
+  if (!sup) return fail(ESEP_EINVAL, "attn_fwd: unsupported dtype / D");
+  return e == hipSuccess ? 0 : hip_fail(e, "attn_fwd launch");
 }
 
 }  // extern "C"

@@ -42,6 +42,8 @@ SIGNATURES = {
                                 _vp, _i32, _vp, _vp, _i32, _i64, _vp, _i64, _vp, _i32, _i64, _i64,
                                 _f32, _vp]),
     "esep_dgamma_reduce": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp]),
+    "esep_attn_fwd": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i32, _i64, _i32,
+                             _i32, _i32, _vp, _i32, _i32, _f32, _vp]),
     "esep_rope": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64,
                          _i32, _i32, _i32, _vp, _i32, _vp, _vp, _i32, _vp, _f32, _vp]),
 }
@@ -279,4 +281,33 @@ def rope(q, k, qo, ko, inv_freq, sign, q_delta=None, positions=None, cu_seqlens=
         dt, B, S, HQ, HK, D, pos_ptr, pos_dt, pos_st, cu_ptr, n_seq,
         inv_freq.data_ptr(), float(sign), _stream(dev))
     _check(rc, "esep_rope")
+    _record(name)
+
+
+def _tokens_ld(t, name):
+    """Token stride of a [T, H, D] tensor whose heads and head dim are packed (stride D, 1)."""
+    if t.dim() != 3 or (t.shape[2] > 1 and t.stride(2) != 1) or (t.shape[1] > 1 and t.stride(1) != t.shape[2]):
+        raise EsepError(f"{name} must be a [T, H, D] tensor with contiguous heads")
+    return t.stride(0)
+
+
+def attn_fwd(q, k, v, o, cu_seqlens, max_seqlen, scale, lse=None, name="_attn_fwd"):
+    """Varlen causal attention forward (esep_attn_fwd). q, o: [T, HQ, D]; k, v: [T, HK, D];
+    cu_seqlens int32 [n_seq + 1] on the device; lse: fp32 [HQ, T] out or None."""
+    dev = _dev(q, k, v, o, cu_seqlens, lse)
+    T, HQ, D = q.shape
+    HK = k.shape[1]
+    if k.shape != (T, HK, D) or v.shape != (T, HK, D) or o.shape != (T, HQ, D):
+        raise EsepError("attention shapes: q, o [T, HQ, D] and k, v [T, HK, D]")
+    if any(t.dtype != q.dtype for t in (k, v, o)):
+        raise EsepError("q, k, v and o must share one dtype")
+    if cu_seqlens.dtype != torch.int32 or not cu_seqlens.is_contiguous():
+        raise EsepError("cu_seqlens must be a contiguous int32 tensor")
+    if lse is not None and (lse.dtype != torch.float32 or not lse.is_contiguous() or lse.shape != (HQ, T)):
+        raise EsepError("lse must be a contiguous fp32 [HQ, T] tensor")
+    rc = lib().esep_attn_fwd(
+        _p(q), _tokens_ld(q, "q"), _p(k), _tokens_ld(k, "k"), _p(v), _tokens_ld(v, "v"),
+        _p(o), _tokens_ld(o, "o"), _p(lse), dtype_code(q.dtype), T, HQ, HK, D, _p(cu_seqlens),
+        cu_seqlens.numel() - 1, int(max_seqlen), float(scale), _stream(dev))
+    _check(rc, "esep_attn_fwd")
     _record(name)

@@ -169,6 +169,27 @@ int esep_rope(const void* q, const int64_t q_strides[3],
               const int32_t* cu_seqlens, int n_seq,
               const float* inv_freq, float sin_sign, void* stream);
 
+/*
+ * Varlen causal attention forward with grouped kv heads, over the packed token layout.
+ * Replaces the per-row scaled_dot_product_attention loop of the reference decoder,
+ * solution/body/packed.py:404-436 (_attention: per original row, is_causal=True,
+ * scale=attn.scaling, query head h reads kv head h / (HQ / HK) as HF's repeat_kv).
+ *
+ *   q [T, HQ, D], k, v [T, HK, D], o [T, HQ, D]    dt (fp16 or bf16), heads of a token
+ *                                                  contiguous, token strides q_rs ... o_rs
+ *   cu_seqlens int32 [n_seq + 1]                   sequence s is tokens [cu[s], cu[s+1]);
+ *                                                  offsets are clamped into [0, T]
+ *   max_seqlen >= every sequence length            (sizes the launch)
+ *   o[t, h] = sum_{j in seq(t), j <= t} softmax_j(scale * q[t, h] . k[j, h']) v[j, h']
+ *   lse [HQ, T] fp32 or NULL                       ln sum_j exp(scale * q . k), for the backward
+ * Fully in fp32 inside (scores, softmax, accumulation); one rounding at the store of o.
+ * No reference C counterpart: the reference calls torch's SDPA once per row.
+ */
+int esep_attn_fwd(const void* q, int64_t q_rs, const void* k, int64_t k_rs, const void* v,
+                  int64_t v_rs, void* o, int64_t o_rs, float* lse, int dt, int64_t T, int HQ,
+                  int HK, int D, const int32_t* cu_seqlens, int n_seq, int max_seqlen,
+                  float scale, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -1,0 +1,91 @@
+"""Varlen causal attention on the GPU (esep_attn_fwd) against the float64 oracle
+(oracle/attention_ref.py), which restates the reference decoder's per-row SDPA loop
+(packed.py:404-436).
+
+Tolerance against the float64 result computed from the same (rounded) inputs: fp16 outputs
+within atol 2e-3 + rtol 1e-2; bf16 outputs within atol 1e-2 + rtol 1e-2 (the probabilities enter
+the P V product in bf16, as in every bf16 flash kernel, so outputs near zero carry ~2^-9 of the
+magnitude of v: torch's own bf16 SDPA misses 2e-3 there too); lse (fp32) within 1e-4. The error
+is also compared with torch's SDPA on the GPU in the same dtype (the reference's kernel): our
+largest error at most twice torch's largest, our mean error at most 1.5 times torch's mean."""
+
+import numpy as np
+import pytest
+import torch
+
+from _util import DEV, gen, np64
+from oracle import attention_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+CASES = [
+    ([1], 2, 2, 64),
+    ([31, 33, 64, 65, 127, 128, 129, 200], 12, 2, 128),
+    ([513, 7], 4, 2, 64),
+    ([300, 1, 257], 28, 4, 128),
+    ([96, 160], 8, 8, 128),
+]
+
+
+def _inputs(lengths, HQ, HK, D, dtype, seed):
+    g = gen(seed)
+    T = int(sum(lengths))
+    q = torch.randn(T, HQ, D, generator=g).to(dtype)
+    k = torch.randn(T, HK, D, generator=g).to(dtype)
+    v = torch.randn(T, HK, D, generator=g).to(dtype)
+    cu = torch.tensor(ref.cu_from_lengths(lengths), dtype=torch.int32)
+    return q.to(DEV), k.to(DEV), v.to(DEV), cu.to(DEV)
+
+
+def _torch_sdpa(q, k, v, lengths, scale):
+    HQ, HK = q.shape[1], k.shape[1]
+    outs = []
+    for qs, ks, vs in zip(q.split(lengths), k.split(lengths), v.split(lengths)):
+        n, D = qs.shape[0], qs.shape[2]
+        qh = qs.reshape(n, HK, HQ // HK, D).permute(1, 2, 0, 3)
+        kh = ks.permute(1, 0, 2).unsqueeze(1).expand(HK, HQ // HK, n, D)
+        vh = vs.permute(1, 0, 2).unsqueeze(1).expand(HK, HQ // HK, n, D)
+        o = torch.nn.functional.scaled_dot_product_attention(qh, kh, vh, is_causal=True, scale=scale)
+        outs.append(o.permute(2, 0, 1, 3).reshape(n, HQ, D))
+    return torch.cat(outs, 0)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_attn_fwd_vs_oracle(case, dtype):
+    from solution.body import _hip
+
+    lengths, HQ, HK, D = CASES[case]
+    q, k, v, cu = _inputs(lengths, HQ, HK, D, dtype, seed=case)
+    T = q.shape[0]
+    scale = D ** -0.5
+    o = torch.full_like(q, float("nan"))
+    lse = torch.full((HQ, T), float("nan"), device=DEV)
+    _hip.attn_fwd(q, k, v, o, cu, max(lengths), scale, lse=lse)
+    o64, lse64 = ref.attn_fwd(np64(q), np64(k), np64(v), cu.cpu().numpy(), scale)
+    err = np.abs(np64(o) - o64)
+    err_t = np.abs(np64(_torch_sdpa(q, k, v, lengths, scale)) - o64)
+    print(f"case {case} {dtype}: max err {err.max():.2e} (torch {err_t.max():.2e}), mean "
+          f"{err.mean():.2e} (torch {err_t.mean():.2e}), lse err {np.abs(np64(lse) - lse64).max():.2e}")
+    atol = 1e-2 if dtype == torch.bfloat16 else 2e-3
+    assert np.all(err <= atol + 1e-2 * np.abs(o64)), err.max()
+    assert err.max() <= 2 * err_t.max() + 1e-6 and err.mean() <= 1.5 * err_t.mean() + 1e-7
+    np.testing.assert_allclose(np64(lse), lse64, atol=1e-4, rtol=1e-5)
+
+
+def test_attn_fwd_sequences_isolated_and_deterministic():
+    """Changing one sequence's keys leaves every other sequence's output bitwise equal; repeated
+    runs are bitwise equal."""
+    from solution.body import _hip
+
+    lengths = [70, 130, 33]
+    q, k, v, cu = _inputs(lengths, 4, 2, 128, torch.bfloat16, seed=11)
+    outs = []
+    for kk in (k, k.clone().index_fill_(0, torch.arange(70, 200, device=DEV), 3.0)):
+        o = torch.empty_like(q)
+        _hip.attn_fwd(q, kk, v, o, cu, 130, 128 ** -0.5)
+        outs.append(o)
+    assert torch.equal(outs[0][:70], outs[1][:70]) and torch.equal(outs[0][200:], outs[1][200:])
+    o2 = torch.empty_like(q)
+    _hip.attn_fwd(q, k, v, o2, cu, 130, 128 ** -0.5)
+    assert torch.equal(outs[0], o2)
