@@ -46,11 +46,121 @@ struct AttnArgs {
   float scale_log2;  // scale * log2(e)
 };
 
-constexpr int kAttnBM = 128;  // queries per block (4 wavefronts x 32)
+// Backward arguments: the forward's plus dO, the saved lse, the per-query delta workspace
+// (fp32 [HQ, T], written by the dQ kernel, read by the dK/dV kernel) and the gradients.
+struct AttnBwdArgs {
+  AttnArgs f;  // q, k, v, o, lse (read), cu, strides, sizes, scale
+  const void* dout;
+  float* delta;  // [HQ, T]
+  void* dq;
+  void* dk;
+  void* dv;
+  int64_t do_rs, dq_rs, dk_rs, dv_rs;
+};
+
+constexpr int kAttnBM = 128;  // queries per forward / dQ block (4 wavefronts x 32)
 constexpr int kAttnBN = 64;   // keys per tile
 constexpr int kAttnThreads = 256;
+constexpr int kAttnBK = 128;  // keys per dK / dV block (4 wavefronts x 32)
+constexpr int kAttnBQ = 64;   // queries per dK / dV tile
 
 hipError_t launch_attn_fwd(const AttnArgs& a, int dt, int D, int max_seqlen, hipStream_t s,
                            bool* supported);
+hipError_t launch_attn_bwd(const AttnBwdArgs& a, int dt, int D, int max_seqlen, hipStream_t s,
+                           bool* supported);
+
+// ---------------------------------------------------------------------------------------
+// Device helpers shared by the attention kernels
+// ---------------------------------------------------------------------------------------
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+
+template <typename T>
+struct Mfma;
+template <>
+struct Mfma<__bf16> {
+  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x16 run(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+  }
+};
+template <>
+struct Mfma<_Float16> {
+  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
+  static __device__ __forceinline__ f32x16 run(v8 a, v8 b, f32x16 c) {
+    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+  }
+};
+
+template <typename V>
+__device__ __forceinline__ V ld16(const void* p) {
+  return __builtin_bit_cast(V, *reinterpret_cast<const uint4*>(p));
+}
+
+// 8 elements from two 4-element (8-byte) halves.
+template <typename V>
+__device__ __forceinline__ V ld8x2(const void* lo, const void* hi) {
+  const uint2 a = *reinterpret_cast<const uint2*>(lo);
+  const uint2 b = *reinterpret_cast<const uint2*>(hi);
+  return __builtin_bit_cast(V, make_uint4(a.x, a.y, b.x, b.y));
+}
+
+// Sequence s's token range [start, end), clamped into [0, T].
+__device__ __forceinline__ void seq_bounds(const int32_t* cu, int s, int64_t T, int* start,
+                                           int* end) {
+  const int tt = (int)T;
+  const int c0 = cu[s], c1 = cu[s + 1];
+  *start = c0 < 0 ? 0 : (c0 > tt ? tt : c0);
+  *end = c1 < *start ? *start : (c1 > tt ? tt : c1);
+}
+
+// Stage a [rows x D] tile (token rows r0 .. r0 + rows - 1 below rend; the rest reads as 0)
+// into LDS row-major with pitch P elements.
+template <typename T, int D, int ROWS, int P>
+__device__ __forceinline__ void stage_rows(T* dst, const T* base, int64_t rs, int r0, int rend,
+                                           int tid) {
+  for (int idx = tid; idx < ROWS * (D / 8); idx += kAttnThreads) {
+    const int r = idx % ROWS, dc = idx / ROWS;
+    uint4 val = make_uint4(0, 0, 0, 0);
+    if (r0 + r < rend) val = *reinterpret_cast<const uint4*>(base + (int64_t)(r0 + r) * rs + 8 * dc);
+    *reinterpret_cast<uint4*>(&dst[r * P + 8 * dc]) = val;
+  }
+}
+
+// Stage the same tile transposed, [D x ROWS] with pitch P: a thread takes rows (2p, 2p + 1) of
+// one 8-column chunk and writes 8 dwords (one per column), each holding the two rows' values.
+template <typename T, int D, int ROWS, int P>
+__device__ __forceinline__ void stage_cols(T* dst, const T* base, int64_t rs, int r0, int rend,
+                                           int tid) {
+  for (int idx = tid; idx < (ROWS / 2) * (D / 8); idx += kAttnThreads) {
+    const int p = idx % (ROWS / 2), dc = idx / (ROWS / 2);
+    const int r = r0 + 2 * p;
+    uint4 v0 = make_uint4(0, 0, 0, 0), v1 = make_uint4(0, 0, 0, 0);
+    if (r < rend) v0 = *reinterpret_cast<const uint4*>(base + (int64_t)r * rs + 8 * dc);
+    if (r + 1 < rend) v1 = *reinterpret_cast<const uint4*>(base + (int64_t)(r + 1) * rs + 8 * dc);
+    const uint32_t w0[4] = {v0.x, v0.y, v0.z, v0.w}, w1[4] = {v1.x, v1.y, v1.z, v1.w};
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      const uint32_t lo = (w0[e / 2] >> (16 * (e % 2))) & 0xffffu;
+      const uint32_t up = (w1[e / 2] >> (16 * (e % 2))) & 0xffffu;
+      *reinterpret_cast<uint32_t*>(&dst[(8 * dc + e) * P + 2 * p]) = lo | (up << 16);
+    }
+  }
+}
+
+// Store a wavefront's [32 tokens x D] result held transposed in MFMA accumulators (acc[md]
+// element 4 j + e is column 32 md + 8 j + 4 hi + e of token `row`), times `mul`.
+template <typename T, int D>
+__device__ __forceinline__ void store_rows_t(T* row, const f32x16 (&acc)[D / 32], int hi,
+                                             float mul) {
+#pragma unroll
+  for (int md = 0; md < D / 32; ++md)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      T o4[4];
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o4[e] = (T)(acc[md][4 * j + e] * mul);
+      *reinterpret_cast<uint2*>(row + 32 * md + 8 * j + 4 * hi) = __builtin_bit_cast(uint2, o4);
+    }
+}
 
 }  // namespace esep

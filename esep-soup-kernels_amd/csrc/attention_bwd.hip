@@ -1,0 +1,263 @@
+// Varlen causal attention backward: two deterministic kernels, no atomics.
+//
+//   P = exp(scale q.k - lse)  (recomputed from the saved lse),   dP = dO V^T,
+//   delta = rowsum(dO * O),   dS = P * (dP - delta),
+//   dQ = scale dS K,   dK = scale dS^T Q,   dV = P^T dO
+//
+// k_attn_bwd_dq: one block per (128 queries, query head) as in the forward. It first computes
+// delta for its queries (stored to the delta workspace), then walks the causal key tiles:
+// S^T = K Q^T and dP^T = V dO^T with the wave's Q and dO held in registers as B operands, and
+// dQ^T += K^T dS^T with K^T staged transposed in LDS and dS^T fed from registers in the permuted
+// key order (the forward's P V trick).
+//
+// k_attn_bwd_dkdv: one block per (128 keys, kv head); wavefront w owns keys 32w..32w+31 and
+// holds their K and V in registers as B operands. It walks, for each query head of the group
+// in turn and each query tile of 64 at or after its keys, S = Q K^T and dP = dO V^T (Q and dO
+// staged row-major in LDS as A operands), then dV^T += dO^T P and dK^T += Q^T dS (Q^T and dO^T
+// staged transposed, P and dS from registers in the permuted query order). Each key's dK and
+// dV are summed by one lane in a fixed order over heads and query tiles, so the result is
+// bitwise reproducible. Runs after k_attn_bwd_dq (it reads delta).
+#include <cmath>
+
+#include "attention.hpp"
+
+namespace esep {
+namespace {
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+template <typename T, int D>
+__global__ __launch_bounds__(kAttnThreads) void k_attn_bwd_dq(const AttnBwdArgs b) {
+  using V8 = typename Mfma<T>::v8;
+  const AttnArgs& a = b.f;
+  constexpr int BN = kAttnBN;
+  constexpr int KP = D + 8;
+  constexpr int TP = BN + 8;
+  __shared__ __align__(16) T ks[BN * KP];  // K row-major (A operand of S^T)
+  __shared__ __align__(16) T vs[BN * KP];  // V row-major (A operand of dP^T)
+  __shared__ __align__(16) T kt_[D * TP];  // K^T (A operand of dQ^T)
+
+  const int seq = blockIdx.z, h = blockIdx.y;
+  int start, end;
+  seq_bounds(a.cu, seq, a.T, &start, &end);
+  const int ntiles = (end - start + kAttnBM - 1) / kAttnBM;
+  if ((int)blockIdx.x >= ntiles) return;
+  const int q0 = start + (ntiles - 1 - (int)blockIdx.x) * kAttnBM;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int lq = lane & 31, hi = lane >> 5;
+  const int kvh = h / (a.HQ / a.HK);
+  const int qw0 = q0 + 32 * w;
+  const int qi = qw0 + lq;
+  const bool qok = qi < end;
+  const bool wave_live = qw0 < end;
+  const int wq_last = qw0 + 31 < end ? qw0 + 31 : end - 1;
+
+  // Q and dO of this lane's query as B operands; delta = dO . O (half per lane, then the pair)
+  V8 qb[D / 16], db[D / 16];
+  float delta = 0.f;
+  {
+    const int64_t col = (int64_t)h * D + 8 * hi;
+    const T* qrow = static_cast<const T*>(a.q) + (int64_t)qi * a.q_rs + col;
+    const T* drow = static_cast<const T*>(b.dout) + (int64_t)qi * b.do_rs + col;
+    const T* orow = static_cast<const T*>(a.o) + (int64_t)qi * a.o_rs + col;
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+      qb[c] = qok ? ld16<V8>(qrow + 16 * c) : V8{};
+      db[c] = qok ? ld16<V8>(drow + 16 * c) : V8{};
+      const V8 o8 = qok ? ld16<V8>(orow + 16 * c) : V8{};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) delta = fmaf((float)db[c][e], (float)o8[e], delta);
+    }
+    delta += __shfl_xor(delta, 32);
+    if (qok && hi == 0) b.delta[(int64_t)h * a.T + qi] = delta;
+  }
+  const float lse2 = qok ? a.lse[(int64_t)h * a.T + qi] * kLog2e : 0.f;
+
+  f32x16 dqa[D / 32];
+#pragma unroll
+  for (int md = 0; md < D / 32; ++md) dqa[md] = f32x16{};
+  const int kend = end < q0 + kAttnBM ? end : q0 + kAttnBM;
+  const T* kbase = static_cast<const T*>(a.k) + (int64_t)kvh * D;
+  const T* vbase = static_cast<const T*>(a.v) + (int64_t)kvh * D;
+
+  for (int kt = start; kt < kend; kt += BN) {
+    __syncthreads();
+    stage_rows<T, D, BN, KP>(ks, kbase, a.k_rs, kt, kend, tid);
+    stage_rows<T, D, BN, KP>(vs, vbase, a.v_rs, kt, kend, tid);
+    stage_cols<T, D, BN, TP>(kt_, kbase, a.k_rs, kt, kend, tid);
+    __syncthreads();
+    if (!wave_live || kt > wq_last) continue;
+
+    V8 dsb[2][2];
+#pragma unroll
+    for (int sb = 0; sb < 2; ++sb) {
+      f32x16 s = f32x16{}, dp = f32x16{};
+      const T* krow = &ks[(32 * sb + lq) * KP + 8 * hi];
+      const T* vrow = &vs[(32 * sb + lq) * KP + 8 * hi];
+#pragma unroll
+      for (int c = 0; c < D / 16; ++c) {
+        s = Mfma<T>::run(ld16<V8>(krow + 16 * c), qb[c], s);
+        dp = Mfma<T>::run(ld16<V8>(vrow + 16 * c), db[c], dp);
+      }
+#pragma unroll
+      for (int i = 0; i < 16; ++i) {
+        const int kj = kt + 32 * sb + 8 * (i / 4) + 4 * hi + (i % 4);
+        const float p = kj <= qi ? exp2f(s[i] * a.scale_log2 - lse2) : 0.f;
+        dsb[sb][i / 8][i % 8] = (T)(p * (dp[i] - delta));
+      }
+    }
+    // dQ^T += K^T dS^T, keys in the permuted order of dsb
+#pragma unroll
+    for (int md = 0; md < D / 32; ++md) {
+      const T* trow = &kt_[(32 * md + lq) * TP + 4 * hi];
+#pragma unroll
+      for (int sb = 0; sb < 2; ++sb)
+#pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2) {
+          const int kb = 32 * sb + 16 * c2;
+          dqa[md] = Mfma<T>::run(ld8x2<V8>(trow + kb, trow + kb + 8), dsb[sb][c2], dqa[md]);
+        }
+    }
+  }
+  if (!qok) return;
+  store_rows_t<T, D>(static_cast<T*>(b.dq) + (int64_t)qi * b.dq_rs + (int64_t)h * D, dqa, hi,
+                     a.scale);
+}
+
+template <typename T, int D>
+__global__ __launch_bounds__(kAttnThreads) void k_attn_bwd_dkdv(const AttnBwdArgs b) {
+  using V8 = typename Mfma<T>::v8;
+  const AttnArgs& a = b.f;
+  constexpr int BQ = kAttnBQ;
+  constexpr int RP = D + 8;   // row-major pitch
+  constexpr int CP = BQ + 8;  // transposed pitch
+  __shared__ __align__(16) T qs[BQ * RP];   // Q row-major (A operand of S)
+  __shared__ __align__(16) T ds_[BQ * RP];  // dO row-major (A operand of dP)
+  __shared__ __align__(16) T qt_[D * CP];   // Q^T (A operand of dK^T)
+  __shared__ __align__(16) T dt_[D * CP];   // dO^T (A operand of dV^T)
+  __shared__ float lse_s[BQ], del_s[BQ];
+
+  const int seq = blockIdx.z, kh = blockIdx.y;
+  int start, end;
+  seq_bounds(a.cu, seq, a.T, &start, &end);
+  const int ntiles = (end - start + kAttnBK - 1) / kAttnBK;
+  if ((int)blockIdx.x >= ntiles) return;
+  const int k0 = start + (int)blockIdx.x * kAttnBK;  // early key tiles see the most queries
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int lq = lane & 31, hi = lane >> 5;
+  const int kw0 = k0 + 32 * w;  // this wavefront's first key
+  const int kj = kw0 + lq;      // this lane's key
+  const bool kok = kj < end;
+  const bool wave_live = kw0 < end;
+  const int G = a.HQ / a.HK;
+
+  // K and V of this lane's key as B operands (B[d][key] = K[key][d]).
+  V8 kb[D / 16], vb[D / 16];
+  {
+    const int64_t col = (int64_t)kh * D + 8 * hi;
+    const T* krow = static_cast<const T*>(a.k) + (int64_t)kj * a.k_rs + col;
+    const T* vrow = static_cast<const T*>(a.v) + (int64_t)kj * a.v_rs + col;
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c) {
+      kb[c] = kok ? ld16<V8>(krow + 16 * c) : V8{};
+      vb[c] = kok ? ld16<V8>(vrow + 16 * c) : V8{};
+    }
+  }
+  f32x16 dka[D / 32], dva[D / 32];
+#pragma unroll
+  for (int md = 0; md < D / 32; ++md) dka[md] = dva[md] = f32x16{};
+
+  for (int g = 0; g < G; ++g) {
+    const int h = kh * G + g;
+    const T* qbase = static_cast<const T*>(a.q) + (int64_t)h * D;
+    const T* dbase = static_cast<const T*>(b.dout) + (int64_t)h * D;
+    for (int qt = k0; qt < end; qt += BQ) {
+      __syncthreads();
+      stage_rows<T, D, BQ, RP>(qs, qbase, a.q_rs, qt, end, tid);
+      stage_rows<T, D, BQ, RP>(ds_, dbase, b.do_rs, qt, end, tid);
+      stage_cols<T, D, BQ, CP>(qt_, qbase, a.q_rs, qt, end, tid);
+      stage_cols<T, D, BQ, CP>(dt_, dbase, b.do_rs, qt, end, tid);
+      if (tid < BQ) {
+        const int t = qt + tid;
+        lse_s[tid] = t < end ? a.lse[(int64_t)h * a.T + t] * kLog2e : 0.f;
+        del_s[tid] = t < end ? b.delta[(int64_t)h * a.T + t] : 0.f;
+      }
+      __syncthreads();
+      // every query of the tile comes before this wave's keys: nothing to add
+      if (!wave_live || qt + BQ - 1 < kw0) continue;
+
+      V8 pb[2][2], sb_[2][2];
+#pragma unroll
+      for (int qh = 0; qh < 2; ++qh) {
+        f32x16 s = f32x16{}, dp = f32x16{};
+        const T* qrow = &qs[(32 * qh + lq) * RP + 8 * hi];
+        const T* drow = &ds_[(32 * qh + lq) * RP + 8 * hi];
+#pragma unroll
+        for (int c = 0; c < D / 16; ++c) {
+          s = Mfma<T>::run(ld16<V8>(qrow + 16 * c), kb[c], s);
+          dp = Mfma<T>::run(ld16<V8>(drow + 16 * c), vb[c], dp);
+        }
+        // s[i] is S[q][kj] for query row r = 32 qh + 8 (i / 4) + 4 hi + i % 4 of the tile
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int r = 32 * qh + 8 * (i / 4) + 4 * hi + (i % 4);
+          const int t = qt + r;
+          const float p = (kj <= t && t < end) ? exp2f(s[i] * a.scale_log2 - lse_s[r]) : 0.f;
+          pb[qh][i / 8][i % 8] = (T)p;
+          sb_[qh][i / 8][i % 8] = (T)(p * (dp[i] - del_s[r]));
+        }
+      }
+      // dV^T += dO^T P and dK^T += Q^T dS, queries in the permuted order of pb / sb_
+#pragma unroll
+      for (int md = 0; md < D / 32; ++md) {
+        const T* drow = &dt_[(32 * md + lq) * CP + 4 * hi];
+        const T* qrow = &qt_[(32 * md + lq) * CP + 4 * hi];
+#pragma unroll
+        for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+          for (int c2 = 0; c2 < 2; ++c2) {
+            const int rb = 32 * qh + 16 * c2;
+            dva[md] = Mfma<T>::run(ld8x2<V8>(drow + rb, drow + rb + 8), pb[qh][c2], dva[md]);
+            dka[md] = Mfma<T>::run(ld8x2<V8>(qrow + rb, qrow + rb + 8), sb_[qh][c2], dka[md]);
+          }
+      }
+    }
+  }
+  if (!kok) return;
+  store_rows_t<T, D>(static_cast<T*>(b.dk) + (int64_t)kj * b.dk_rs + (int64_t)kh * D, dka, hi,
+                     a.scale);
+  store_rows_t<T, D>(static_cast<T*>(b.dv) + (int64_t)kj * b.dv_rs + (int64_t)kh * D, dva, hi,
+                     1.f);
+}
+
+template <typename T, int D>
+hipError_t bwd_run(const AttnBwdArgs& b, int max_seqlen, hipStream_t s) {
+  const dim3 gq((max_seqlen + kAttnBM - 1) / kAttnBM, b.f.HQ, b.f.n_seq);
+  hipLaunchKernelGGL((k_attn_bwd_dq<T, D>), gq, dim3(kAttnThreads), 0, s, b);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  const dim3 gk((max_seqlen + kAttnBK - 1) / kAttnBK, b.f.HK, b.f.n_seq);
+  hipLaunchKernelGGL((k_attn_bwd_dkdv<T, D>), gk, dim3(kAttnThreads), 0, s, b);
+  return hipGetLastError();
+}
+
+template <typename T>
+hipError_t bwd_d(const AttnBwdArgs& b, int D, int max_seqlen, hipStream_t s, bool* sup) {
+  *sup = true;
+  if (D == 128) return bwd_run<T, 128>(b, max_seqlen, s);
+  if (D == 64) return bwd_run<T, 64>(b, max_seqlen, s);
+  *sup = false;
+  return hipErrorInvalidValue;
+}
+
+}  // namespace
+
+hipError_t launch_attn_bwd(const AttnBwdArgs& b, int dt, int D, int max_seqlen, hipStream_t s,
+                           bool* sup) {
+  if (dt == 1) return bwd_d<_Float16>(b, D, max_seqlen, s, sup);
+  if (dt == 2) return bwd_d<__bf16>(b, D, max_seqlen, s, sup);
+  *sup = false;
+  return hipErrorInvalidValue;
+}
+
+}  // namespace esep

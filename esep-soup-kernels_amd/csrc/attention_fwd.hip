@@ -6,38 +6,6 @@
 namespace esep {
 namespace {
 
-typedef float f32x16 __attribute__((ext_vector_type(16)));
-
-template <typename T>
-struct Mfma;
-template <>
-struct Mfma<__bf16> {
-  typedef __bf16 v8 __attribute__((ext_vector_type(8)));
-  static __device__ __forceinline__ f32x16 run(v8 a, v8 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
-  }
-};
-template <>
-struct Mfma<_Float16> {
-  typedef _Float16 v8 __attribute__((ext_vector_type(8)));
-  static __device__ __forceinline__ f32x16 run(v8 a, v8 b, f32x16 c) {
-    return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
-  }
-};
-
-template <typename V>
-__device__ __forceinline__ V ld16(const void* p) {
-  return __builtin_bit_cast(V, *reinterpret_cast<const uint4*>(p));
-}
-
-// 8 elements from two 4-element (8-byte) halves.
-template <typename V>
-__device__ __forceinline__ V ld8x2(const void* lo, const void* hi) {
-  const uint2 a = *reinterpret_cast<const uint2*>(lo);
-  const uint2 b = *reinterpret_cast<const uint2*>(hi);
-  return __builtin_bit_cast(V, make_uint4(a.x, a.y, b.x, b.y));
-}
-
 template <typename T, int D>
 __global__ __launch_bounds__(kAttnThreads) void k_attn_fwd(const AttnArgs a) {
   using V8 = typename Mfma<T>::v8;
@@ -48,11 +16,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_fwd(const AttnArgs a) {
   __shared__ __align__(16) T vt[D * VP];
 
   const int seq = blockIdx.z, h = blockIdx.y;
-  // sequence bounds, clamped into [0, T] so that malformed offsets stay in bounds
-  const int tt = (int)a.T;
-  const int c0 = a.cu[seq], c1 = a.cu[seq + 1];
-  const int start = c0 < 0 ? 0 : (c0 > tt ? tt : c0);
-  const int end = c1 < start ? start : (c1 > tt ? tt : c1);
+  int start, end;  // clamped into [0, T]: malformed offsets stay in bounds
+  seq_bounds(a.cu, seq, a.T, &start, &end);
   const int ntiles = (end - start + kAttnBM - 1) / kAttnBM;
   if ((int)blockIdx.x >= ntiles) return;
   const int q0 = start + (ntiles - 1 - (int)blockIdx.x) * kAttnBM;  // heaviest tiles first
@@ -83,30 +48,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_fwd(const AttnArgs a) {
 
   for (int kt = start; kt < kend; kt += BN) {
     __syncthreads();  // the previous tile's LDS reads are done
-    // K tile, row-major: 64 keys x D/8 chunks of 16 bytes (keys past kend read as 0).
-    for (int idx = tid; idx < BN * (D / 8); idx += kAttnThreads) {
-      const int key = idx % BN, dc = idx / BN;
-      uint4 val = make_uint4(0, 0, 0, 0);
-      if (kt + key < kend)
-        val = *reinterpret_cast<const uint4*>(kbase + (int64_t)(kt + key) * a.k_rs + 8 * dc);
-      *reinterpret_cast<uint4*>(&ks[key * KP + 8 * dc]) = val;
-    }
-    // V^T tile: a thread takes keys (2p, 2p + 1) of one 8-column chunk and writes 8 dwords
-    // (one per column d), each holding the two keys' values.
-    for (int idx = tid; idx < (BN / 2) * (D / 8); idx += kAttnThreads) {
-      const int p = idx % (BN / 2), dc = idx / (BN / 2);
-      const int kj = kt + 2 * p;
-      uint4 v0 = make_uint4(0, 0, 0, 0), v1 = make_uint4(0, 0, 0, 0);
-      if (kj < kend) v0 = *reinterpret_cast<const uint4*>(vbase + (int64_t)kj * a.v_rs + 8 * dc);
-      if (kj + 1 < kend) v1 = *reinterpret_cast<const uint4*>(vbase + (int64_t)(kj + 1) * a.v_rs + 8 * dc);
-      const uint32_t w0[4] = {v0.x, v0.y, v0.z, v0.w}, w1[4] = {v1.x, v1.y, v1.z, v1.w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t lo = (w0[e / 2] >> (16 * (e % 2))) & 0xffffu;
-        const uint32_t up = (w1[e / 2] >> (16 * (e % 2))) & 0xffffu;
-        *reinterpret_cast<uint32_t*>(&vt[(8 * dc + e) * VP + 2 * p]) = lo | (up << 16);
-      }
-    }
+    stage_rows<T, D, BN, KP>(ks, kbase, a.k_rs, kt, kend, tid);  // keys past kend read 0
+    stage_cols<T, D, BN, VP>(vt, vbase, a.v_rs, kt, kend, tid);  // V^T
     __syncthreads();
     if (!wave_live || kt > wq_last) continue;  // every key of the tile is after this wave's queries
 
@@ -166,17 +109,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_fwd(const AttnArgs a) {
 
   if (!wave_live || qi >= end) return;
   // O = O^T / l: lane (lq, hi) holds columns d = 32 md + 8 j + 4 hi + (0..3) of query qi.
-  const float inv = l > 0.f ? 1.f / l : 0.f;
-  T* orow = static_cast<T*>(a.o) + (int64_t)qi * a.o_rs + (int64_t)h * D + 4 * hi;
-#pragma unroll
-  for (int md = 0; md < D / 32; ++md)
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      T o4[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o4[e] = (T)(oacc[md][4 * j + e] * inv);
-      *reinterpret_cast<uint2*>(orow + 32 * md + 8 * j) = __builtin_bit_cast(uint2, o4);
-    }
+  store_rows_t<T, D>(static_cast<T*>(a.o) + (int64_t)qi * a.o_rs + (int64_t)h * D, oacc, hi,
+                     l > 0.f ? 1.f / l : 0.f);
   if (hi == 0 && a.lse != nullptr)
     a.lse[(int64_t)h * a.T + qi] = (m + log2f(l)) * 0.69314718055994531f;
 }

@@ -397,4 +397,65 @@ int esep_attn_fwd(const void* q, int64_t q_rs, const void* k, int64_t k_rs, cons
   return e == hipSuccess ? 0 : hip_fail(e, "attn_fwd launch");
 }
 
+int esep_attn_bwd(const void* q, int64_t q_rs, const void* k, int64_t k_rs, const void* v,
+                  int64_t v_rs, const void* o, int64_t o_rs, const void* dout, int64_t do_rs,
+                  const float* lse, float* delta, void* dq, int64_t dq_rs, void* dk,
+                  int64_t dk_rs, void* dv, int64_t dv_rs, int dt, int64_t T, int HQ, int HK,
+                  int D, const int32_t* cu_seqlens, int n_seq, int max_seqlen, float scale,
+                  void* stream) {
+  g_err[0] = 0;
+  if (dt != ESEP_F16 && dt != ESEP_BF16)
+    return fail(ESEP_EINVAL, "attn_bwd: dtype %d is not fp16 / bf16", dt);
+  if (D != 64 && D != 128) return fail(ESEP_ESHAPE, "attn_bwd: D=%d not in {64, 128}", D);
+  if (T < 0 || T > 0x7fffffff || HQ < 1 || HK < 1 || HQ % HK != 0 || n_seq < 0 || max_seqlen < 0)
+    return fail(ESEP_ESHAPE, "attn_bwd: bad sizes T=%lld HQ=%d HK=%d n_seq=%d max_seqlen=%d",
+                (long long)T, HQ, HK, n_seq, max_seqlen);
+  const int64_t wq = (int64_t)HQ * D, wk = (int64_t)HK * D;
+  if (q_rs < wq || o_rs < wq || do_rs < wq || dq_rs < wq || k_rs < wk || v_rs < wk ||
+      dk_rs < wk || dv_rs < wk)
+    return fail(ESEP_ESHAPE, "attn_bwd: token stride smaller than heads * D");
+  if (T == 0 || n_seq == 0 || max_seqlen == 0) return 0;
+  const void* ptrs[] = {q, k, v, o, dout, dq, dk, dv};
+  for (const void* p : ptrs)
+    if (p == nullptr) return fail(ESEP_EINVAL, "attn_bwd: q, k, v, o, dout, dq, dk, dv are required");
+  if (lse == nullptr || delta == nullptr || cu_seqlens == nullptr)
+    return fail(ESEP_EINVAL, "attn_bwd: lse, the delta workspace and cu_seqlens are required");
+  const int64_t rss[] = {q_rs, k_rs, v_rs, o_rs, do_rs, dq_rs, dk_rs, dv_rs};
+  for (int i = 0; i < 8; ++i)
+    if (!aligned16(ptrs[i]) || (rss[i] & 7))
+      return fail(ESEP_EALIGN, "attn_bwd: tensors need 16-byte alignment and token strides "
+                               "that are multiples of 8 elements");
+  if (!(scale > 0.f)) return fail(ESEP_EINVAL, "attn_bwd: scale must be positive");
+  esep::AttnBwdArgs b{};
+  b.f.q = q;
+  b.f.k = k;
+  b.f.v = v;
+  b.f.o = const_cast<void*>(o);
+  b.f.lse = const_cast<float*>(lse);
+  b.f.cu = cu_seqlens;
+  b.f.q_rs = q_rs;
+  b.f.k_rs = k_rs;
+  b.f.v_rs = v_rs;
+  b.f.o_rs = o_rs;
+  b.f.T = T;
+  b.f.n_seq = n_seq;
+  b.f.HQ = HQ;
+  b.f.HK = HK;
+  b.f.scale = scale;
+  b.f.scale_log2 = scale * 1.4426950408889634f;
+  b.dout = dout;
+  b.delta = delta;
+  b.dq = dq;
+  b.dk = dk;
+  b.dv = dv;
+  b.do_rs = do_rs;
+  b.dq_rs = dq_rs;
+  b.dk_rs = dk_rs;
+  b.dv_rs = dv_rs;
+  bool sup = false;
+  const hipError_t e = esep::launch_attn_bwd(b, dt, D, max_seqlen, static_cast<hipStream_t>(stream), &sup);
+  if (!sup) return fail(ESEP_EINVAL, "attn_bwd: unsupported dtype / D");
+  return e == hipSuccess ? 0 : hip_fail(e, "attn_bwd launch");
+}
+
 }  // extern "C"

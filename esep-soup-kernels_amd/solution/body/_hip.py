@@ -44,6 +44,9 @@ SIGNATURES = {
     "esep_dgamma_reduce": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp]),
     "esep_attn_fwd": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i32, _i64, _i32,
                              _i32, _i32, _vp, _i32, _i32, _f32, _vp]),
+    "esep_attn_bwd": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp,
+                             _vp, _i64, _vp, _i64, _vp, _i64, _i32, _i64, _i32, _i32, _i32, _vp,
+                             _i32, _i32, _f32, _vp]),
     "esep_rope": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64,
                          _i32, _i32, _i32, _vp, _i32, _vp, _vp, _i32, _vp, _f32, _vp]),
 }
@@ -310,4 +313,33 @@ def attn_fwd(q, k, v, o, cu_seqlens, max_seqlen, scale, lse=None, name="_attn_fw
         _p(o), _tokens_ld(o, "o"), _p(lse), dtype_code(q.dtype), T, HQ, HK, D, _p(cu_seqlens),
         cu_seqlens.numel() - 1, int(max_seqlen), float(scale), _stream(dev))
     _check(rc, "esep_attn_fwd")
+    _record(name)
+
+
+def attn_bwd(q, k, v, o, dout, lse, dq, dk, dv, cu_seqlens, max_seqlen, scale, delta=None,
+             name="_attn_bwd"):
+    """Backward of attn_fwd (esep_attn_bwd): dq [T, HQ, D], dk, dv [T, HK, D] out. `delta` is
+    the fp32 [HQ, T] workspace (allocated here when not given)."""
+    dev = _dev(q, k, v, o, dout, lse, dq, dk, dv, cu_seqlens, delta)
+    T, HQ, D = q.shape
+    HK = k.shape[1]
+    for t, shp in ((o, (T, HQ, D)), (dout, (T, HQ, D)), (dq, (T, HQ, D)), (k, (T, HK, D)),
+                   (v, (T, HK, D)), (dk, (T, HK, D)), (dv, (T, HK, D))):
+        if tuple(t.shape) != shp or t.dtype != q.dtype:
+            raise EsepError("attention backward shapes / dtypes do not match q [T, HQ, D], k [T, HK, D]")
+    if lse.dtype != torch.float32 or not lse.is_contiguous() or tuple(lse.shape) != (HQ, T):
+        raise EsepError("lse must be a contiguous fp32 [HQ, T] tensor")
+    if cu_seqlens.dtype != torch.int32 or not cu_seqlens.is_contiguous():
+        raise EsepError("cu_seqlens must be a contiguous int32 tensor")
+    if delta is None:
+        delta = torch.empty((HQ, T), device=dev, dtype=torch.float32)
+    elif delta.dtype != torch.float32 or not delta.is_contiguous() or tuple(delta.shape) != (HQ, T):
+        raise EsepError("delta must be a contiguous fp32 [HQ, T] tensor")
+    rc = lib().esep_attn_bwd(
+        _p(q), _tokens_ld(q, "q"), _p(k), _tokens_ld(k, "k"), _p(v), _tokens_ld(v, "v"),
+        _p(o), _tokens_ld(o, "o"), _p(dout), _tokens_ld(dout, "dout"), _p(lse), _p(delta),
+        _p(dq), _tokens_ld(dq, "dq"), _p(dk), _tokens_ld(dk, "dk"), _p(dv), _tokens_ld(dv, "dv"),
+        dtype_code(q.dtype), T, HQ, HK, D, _p(cu_seqlens), cu_seqlens.numel() - 1,
+        int(max_seqlen), float(scale), _stream(dev))
+    _check(rc, "esep_attn_bwd")
     _record(name)

@@ -17,9 +17,12 @@ kernel takes, as the reference's do):
               deterministic two-stage reduction (the reference sends it to HF, packed.py:129).
   _rope       norm_rope.rope on the packed positions and the model's inv_freq (HF default rope
               type with attention_scaling 1.0), fp16 / bf16 / fp32 q and k.
-The rest of the layer (q/k/v/o projections, per-row SDPA attention, MLP) calls the model's own
-modules: the reference's NF4 / LoRA / recompute-MLP routes (packed.py:184-352, :440-693) are
-other workstreams and are not part of this build; their flags exist for API compatibility.
+  _attention  attention.varlen_attention: causal attention over all rows in one launch per
+              direction (fp16 / bf16, head_dim 64 or 128, no dropout); else the reference's
+              per-row SDPA loop.
+The rest of the layer (q/k/v/o projections, MLP) calls the model's own modules: the
+reference's NF4 / LoRA / recompute-MLP routes (packed.py:184-352, :440-693) are other
+workstreams and are not part of this build; their flags exist for API compatibility.
 """
 
 import contextlib
@@ -187,16 +190,40 @@ def _rope(q, k, rope_in, q_delta=None):
     return apply_rotary_pos_emb(q, k, cos, sin, unsqueeze_dim=2)
 
 
+_CU_CACHE = {}  # (device, lens) -> cu_seqlens of the current batch (one entry)
+
+
+def _cu_seqlens(lens, device):
+    key = (device, tuple(lens))
+    cu = _CU_CACHE.get(key)
+    if cu is None:
+        from .attention import cu_seqlens_from_lengths
+
+        _CU_CACHE.clear()
+        cu = _CU_CACHE[key] = cu_seqlens_from_lengths(lens, device)
+    return cu
+
+
 def _attention(attn, q, k, v, lens):
     """Causal attention per original row on its packed slice. q [1, T, Hq, D], k/v [1, T, Hk, D]
-    -> [1, T, Hq * D]. GQA: query head h uses kv head h // (Hq / Hk), as HF's repeat_kv; the kv
-    heads are broadcast with a zero stride instead of copied."""
+    -> [1, T, Hq * D]. GQA: query head h uses kv head h // (Hq / Hk), as HF's repeat_kv.
+    With the kernels on (fp16 / bf16, D in {64, 128}, no dropout) every row runs in one varlen
+    launch (attention.varlen_attention); otherwise per row through torch's SDPA with the kv
+    heads broadcast by a zero stride (reference packed.py:404-436)."""
     if torch.is_autocast_enabled("cuda"):
         dt = torch.get_autocast_dtype("cuda")
         q, k, v = q.to(dt), k.to(dt), v.to(dt)
     hq, hk, d = q.shape[2], k.shape[2], q.shape[3]
     groups = hq // hk
     dropout = attn.attention_dropout if attn.training else 0.0
+    if USE_KERNELS:
+        from . import attention
+
+        if attention.supported(q, k, v, dropout):
+            o = attention.varlen_attention(q, k, v, _cu_seqlens(lens, q.device), max(lens),
+                                           attn.scaling)
+            return o.view(1, o.shape[0], hq * d)
+        _fallback("attention kernel", f"dtype {q.dtype}, head_dim {d}, dropout {dropout}")
     outs = []
     for qr, kr, vr in zip(q.squeeze(0).split(lens), k.squeeze(0).split(lens),
                           v.squeeze(0).split(lens)):

@@ -190,6 +190,24 @@ int esep_attn_fwd(const void* q, int64_t q_rs, const void* k, int64_t k_rs, cons
                   int HK, int D, const int32_t* cu_seqlens, int n_seq, int max_seqlen,
                   float scale, void* stream);
 
+/*
+ * Backward of esep_attn_fwd (same layout and argument meanings), deterministic (no atomics).
+ * Replaces the autograd backward of the reference's per-row SDPA calls (packed.py:428-429).
+ *
+ *   o, lse    the forward's output and its saved lse
+ *   dout      [T, HQ, D] gradient of o
+ *   delta     fp32 [HQ, T] workspace (caller-allocated; rowsum(dout * o), written then read)
+ *   dq [T, HQ, D], dk, dv [T, HK, D]   outputs in dt; dk and dv sum over the query heads of
+ *                                      their group in a fixed order
+ * Two kernels on the stream: dQ (and delta) per query tile, then dK and dV per key tile.
+ */
+int esep_attn_bwd(const void* q, int64_t q_rs, const void* k, int64_t k_rs, const void* v,
+                  int64_t v_rs, const void* o, int64_t o_rs, const void* dout, int64_t do_rs,
+                  const float* lse, float* delta, void* dq, int64_t dq_rs, void* dk,
+                  int64_t dk_rs, void* dv, int64_t dv_rs, int dt, int64_t T, int HQ, int HK,
+                  int D, const int32_t* cu_seqlens, int n_seq, int max_seqlen, float scale,
+                  void* stream);
+
 #ifdef __cplusplus
 }
 #endif

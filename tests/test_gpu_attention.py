@@ -89,3 +89,58 @@ def test_attn_fwd_sequences_isolated_and_deterministic():
     o2 = torch.empty_like(q)
     _hip.attn_fwd(q, k, v, o2, cu, 130, 128 ** -0.5)
     assert torch.equal(outs[0], o2)
+
+
+def _torch_grads(q, k, v, do, lengths, scale):
+    qq, kk, vv = (t.detach().clone().requires_grad_() for t in (q, k, v))
+    o = _torch_sdpa(qq, kk, vv, lengths, scale)
+    return torch.autograd.grad(o, [qq, kk, vv], do)
+
+
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16], ids=["bf16", "fp16"])
+@pytest.mark.parametrize("case", range(len(CASES)))
+def test_attn_bwd_vs_oracle(case, dtype):
+    """dq, dk, dv against the float64 closed form (oracle.attn_bwd) and torch's autograd SDPA in
+    the same dtype: each gradient's error is within 1e-2 (bf16) / 2e-3 (fp16) of its largest
+    magnitude plus 1e-2 relative (plus 1e-5 absolute), its largest error at most twice
+    torch's, its mean error at most 1.5 times torch's."""
+    from solution.body import _hip
+
+    lengths, HQ, HK, D = CASES[case]
+    q, k, v, cu = _inputs(lengths, HQ, HK, D, dtype, seed=100 + case)
+    do = torch.randn(q.shape, generator=gen(200 + case)).to(dtype).to(DEV)
+    scale = D ** -0.5
+    o = torch.empty_like(q)
+    lse = torch.empty((HQ, q.shape[0]), device=DEV)
+    _hip.attn_fwd(q, k, v, o, cu, max(lengths), scale, lse=lse)
+    dq, dk, dv = (torch.full_like(t, float("nan")) for t in (q, k, v))
+    _hip.attn_bwd(q, k, v, o, do, lse, dq, dk, dv, cu, max(lengths), scale)
+    want = ref.attn_bwd(np64(q), np64(k), np64(v), np64(do), cu.cpu().numpy(), scale)
+    tg = _torch_grads(q, k, v, do, lengths, scale)
+    atol = 1e-2 if dtype == torch.bfloat16 else 2e-3
+    for name, got, w64, t in zip(("dq", "dk", "dv"), (dq, dk, dv), want, tg):
+        err = np.abs(np64(got) - w64)
+        err_t = np.abs(np64(t) - w64)
+        print(f"case {case} {dtype} {name}: max err {err.max():.2e} (torch {err_t.max():.2e}), "
+              f"mean {err.mean():.2e} (torch {err_t.mean():.2e}), max |g| {np.abs(w64).max():.2e}")
+        # (+1e-5: a one-token sequence's exact dq is 0, and both kernels leave rounding there)
+        assert np.all(err <= atol * np.abs(w64).max() + 1e-2 * np.abs(w64) + 1e-5), (name, err.max())
+        assert err.max() <= 2 * err_t.max() + 1e-6, (name, err.max(), err_t.max())
+        assert err.mean() <= 1.5 * err_t.mean() + 1e-7, (name, err.mean(), err_t.mean())
+
+
+def test_attn_bwd_deterministic():
+    from solution.body import _hip
+
+    lengths = [300, 45]
+    q, k, v, cu = _inputs(lengths, 12, 2, 128, torch.bfloat16, seed=21)
+    do = torch.randn(q.shape, generator=gen(22)).to(torch.bfloat16).to(DEV)
+    o = torch.empty_like(q)
+    lse = torch.empty((12, q.shape[0]), device=DEV)
+    _hip.attn_fwd(q, k, v, o, cu, 300, 128 ** -0.5, lse=lse)
+    runs = []
+    for _ in range(2):
+        g = [torch.empty_like(t) for t in (q, k, v)]
+        _hip.attn_bwd(q, k, v, o, do, lse, *g, cu, 300, 128 ** -0.5)
+        runs.append(g)
+    assert all(torch.equal(a, b) for a, b in zip(*runs))

@@ -1,5 +1,5 @@
 """The packed-decoder patch point on the GPU: a tiny random Qwen2 through the patched
-Qwen2Model.forward (HIP norms and RoPE) against HF's original forward, restating the reference's
+Qwen2Model.forward (HIP norms, RoPE and varlen attention) against HF's original forward, restating the reference's
 solution/test_body_packed.py (:20-338): hidden states, loss and every gradient within the
 reference's tolerances, pad positions exactly zero, launch counts by kernel name, and the
 guarded fallbacks. peft / bitsandbytes are not installed, so the reference's "lora" and
@@ -107,7 +107,8 @@ def _compare(ref, new, mask, tol_h=5e-3, tol_loss=1e-3, tol_g=2e-2):
 
 
 def _counts(names):
-    return {k: names.count(k) for k in ("_add_rmsnorm_fwd", "_add_rmsnorm_bwd", "_rope_kernel")}
+    return {k: names.count(k) for k in ("_add_rmsnorm_fwd", "_add_rmsnorm_bwd", "_rope_kernel",
+                                        "_attn_fwd", "_attn_bwd")}
 
 
 @pytest.mark.parametrize("kernels", [True, False], ids=["kernels", "torch"])
@@ -136,6 +137,8 @@ def test_packed_matches_original(variant, left, kernels, dtype):
         assert c["_add_rmsnorm_fwd"] == 2 * norms, c  # loss forward + hidden forward
         assert c["_add_rmsnorm_bwd"] == norm_bwd, c
         assert c["_rope_kernel"] == 3 * n_layers, c
+        # one varlen attention launch per layer and direction (loss forward + hidden forward)
+        assert c["_attn_fwd"] == 2 * n_layers and c["_attn_bwd"] == n_layers, c
     else:
         assert not any(c.values()), c
 
