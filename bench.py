@@ -24,6 +24,7 @@ cores on one layer of the same workload.
 """
 
 import argparse
+import itertools
 import json
 import os
 import statistics
@@ -330,6 +331,92 @@ def run_api_variant(dev, reps, n_sets=6):
             "kernels": out}
 
 
+def attn_flops(lengths, HQ, D):
+    """Algorithmic causal attention FLOPs: (forward, backward). Each (query, key <= query) pair
+    of a head costs 2 D multiply-adds per product: QK^T and PV forward (4 D), S, dP, dV, dK, dQ
+    backward (10 D)."""
+    pairs = sum(n * (n + 1) // 2 for n in lengths)
+    return 4 * D * HQ * pairs, 10 * D * HQ * pairs
+
+
+PEAK_BF16_TFLOPS = 2500.0
+
+
+def run_attention(dev, reps):
+    """The varlen causal attention kernels (esep_attn_fwd / esep_attn_bwd, bf16) at the config-4
+    shape (8 rows of 1024, 12/2 heads) and the config-5 shape (29 packed sequences, 28/4 heads),
+    graphed and timed with HIP events, beside the reference's per-row SDPA loop
+    (packed.py:404-436, torch's scaled_dot_product_attention on the same GPU, eager)."""
+    import torch
+
+    from solution.body import _hip
+
+    out = {}
+    for name, lengths, HQ, HK in (("config4", [CFG4["S"]] * CFG4["B"], CFG4["HQ"], CFG4["HK"]),
+                                  ("config5", config5_lengths(CFG5), CFG5["HQ"], CFG5["HK"])):
+        D = 128
+        T = sum(lengths)
+        g = torch.Generator(device=dev).manual_seed(11)
+        bf = torch.bfloat16
+
+        def rn(*shape):
+            return torch.randn(shape, generator=g, device=dev, dtype=torch.float32).to(bf)
+
+        q, k, v, do = rn(T, HQ, D), rn(T, HK, D), rn(T, HK, D), rn(T, HQ, D)
+        o, dq, dk, dv = torch.empty_like(q), torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+        lse = torch.empty(HQ, T, device=dev)
+        ws = torch.empty(_hip.attn_bwd_workspace(T, HQ, HK, D), device=dev)
+        cu = torch.tensor([0] + list(itertools.accumulate(lengths)), dtype=torch.int32, device=dev)
+        L, scale = max(lengths), D ** -0.5
+        fwd = lambda: _hip.attn_fwd(q, k, v, o, cu, L, scale, lse=lse)
+        bwd = lambda: _hip.attn_bwd(q, k, v, o, do, lse, dq, dk, dv, cu, L, scale, workspace=ws)
+        ff, fb = attn_flops(lengths, HQ, D)
+        res = {"tokens": T, "sequences": len(lengths), "heads": f"{HQ}/{HK}", "head_dim": D}
+        for kind, fn, fl in (("fwd", fwd, ff), ("bwd", bwd, fb)):
+            gr = capture(fn)
+            time_graph(gr, 2)
+            ms, _ = time_graph(gr, reps)
+            tf = fl / (ms * 1e-3) / 1e12
+            res[kind] = {"ms": round(ms, 4), "TFLOP/s": round(tf, 1), "frac": round(tf / PEAK_BF16_TFLOPS, 4)}
+            log(f"attention {name} {kind}: {ms:.3f} ms, {tf:.0f} TFLOP/s = {tf / PEAK_BF16_TFLOPS:.1%} of bf16 MFMA peak")
+            del gr
+        # the reference's per-row loop, forward + backward, eager
+        qr, kr, vr = (t.detach().clone().requires_grad_() for t in (q, k, v))
+
+        def ref_step():
+            outs = []
+            for qs, ks, vs in zip(qr.split(lengths), kr.split(lengths), vr.split(lengths)):
+                n = qs.shape[0]
+                qh = qs.reshape(n, HK, HQ // HK, D).permute(1, 2, 0, 3)
+                kh = ks.permute(1, 0, 2).unsqueeze(1).expand(HK, HQ // HK, n, D)
+                vh = vs.permute(1, 0, 2).unsqueeze(1).expand(HK, HQ // HK, n, D)
+                oo = torch.nn.functional.scaled_dot_product_attention(qh, kh, vh, is_causal=True, scale=scale)
+                outs.append(oo.permute(2, 0, 1, 3))
+            torch.autograd.backward(torch.cat(outs, 0), do.view(T, HK, HQ // HK, D))
+
+        ref_step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        n_ref = max(3, reps // 4)
+        e0.record()
+        for _ in range(n_ref):
+            ref_step()
+        e1.record()
+        torch.cuda.synchronize()
+        ref_ms = e0.elapsed_time(e1) / n_ref
+        ours = res["fwd"]["ms"] + res["bwd"]["ms"]
+        res["reference_loop_fwd_bwd_ms"] = round(ref_ms, 4)
+        res["speedup_vs_reference_loop"] = round(ref_ms / ours, 2)
+        log(f"attention {name}: fwd+bwd {ours:.3f} ms vs the reference's per-row SDPA loop {ref_ms:.3f} ms")
+        out[name] = res
+        del q, k, v, do, o, dq, dk, dv, lse, ws, qr, kr, vr
+        torch.cuda.empty_cache()
+    return {"workload": "varlen causal GQA attention, bf16, head_dim 128, fwd (o, lse) and bwd "
+                        "(dq, dk, dv): config4 = 8 rows of 1024 tokens, 12/2 heads; config5 = the "
+                        "29 packed sequences of config 5, 28/4 heads",
+            "peak_TFLOP/s": PEAK_BF16_TFLOPS, **out}
+
+
 def kernel_rooflines(body, reps):
     """Per-launch time of each entry point: a graph of one launch per layer of that kernel
     alone (distinct tensors, as in the sweep), replayed `reps` times, timed with HIP events
@@ -408,6 +495,7 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline leg")
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--no-config5", action="store_true", help="skip the config 5 stress line")
+    ap.add_argument("--no-attention", action="store_true", help="skip the attention measurement")
     ap.add_argument("--pmc-kernel", choices=["rmsnorm_fwd", "rmsnorm_bwd", "rope_fwd", "rope_bwd"],
                     help="counter-collection run: a calibration copy of 256 MiB (read 256 MiB, "
                          "write 256 MiB) three times, then one launch per layer of this kernel "
@@ -481,6 +569,7 @@ def main():
     torch.cuda.empty_cache()
     c5 = None if args.no_config5 else run_config5(dev, max(args.steps // 3, 5))
     api = run_api_variant(dev, max(args.steps // 3, 5))
+    attn = None if args.no_attention else run_attention(dev, max(args.steps // 3, 5))
 
     cpu = None
     if not args.no_cpu:
@@ -508,6 +597,7 @@ def main():
         "cpu_baseline": cpu,
         "config5": c5,
         "api_variant": api,
+        "attention": attn,
     }
     print(json.dumps(out), flush=True)
     return 0

@@ -46,16 +46,19 @@ struct AttnArgs {
   float scale_log2;  // scale * log2(e)
 };
 
-// Backward arguments: the forward's plus dO, the saved lse, the per-query delta workspace
-// (fp32 [HQ, T], written by the dQ kernel, read by the dK/dV kernel) and the gradients.
+// Backward arguments: the forward's plus dO, the saved lse, the workspace (per-query delta,
+// fp32 [HQ, T], written by the dQ kernel and read by the dK/dV kernel; then the dK / dV partials
+// when the query heads of a kv head are split over blocks) and the gradients.
 struct AttnBwdArgs {
   AttnArgs f;  // q, k, v, o, lse (read), cu, strides, sizes, scale
   const void* dout;
   float* delta;  // [HQ, T]
+  float* part;   // [2][split][T][HK][D] fp32 dK / dV partials (split > 1)
   void* dq;
   void* dk;
   void* dv;
   int64_t do_rs, dq_rs, dk_rs, dv_rs;
+  int split;  // blocks per kv head and key tile (a divisor of HQ / HK)
 };
 
 constexpr int kAttnBM = 128;  // queries per forward / dQ block (4 wavefronts x 32)

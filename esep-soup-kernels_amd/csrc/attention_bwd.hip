@@ -10,13 +10,16 @@
 // dQ^T += K^T dS^T with K^T staged transposed in LDS and dS^T fed from registers in the permuted
 // key order (the forward's P V trick).
 //
-// k_attn_bwd_dkdv: one block per (128 keys, kv head); wavefront w owns keys 32w..32w+31 and
-// holds their K and V in registers as B operands. It walks, for each query head of the group
-// in turn and each query tile of 64 at or after its keys, S = Q K^T and dP = dO V^T (Q and dO
+// k_attn_bwd_dkdv: one block per (128 keys, kv head, part of the kv head's query heads);
+// wavefront w owns keys 32w..32w+31 and holds their K and V in registers as B operands. It
+// walks, for each of its query heads in turn and each query tile of 64 at or after its keys
+// (the next tile prefetched into registers during the current one), S = Q K^T and dP = dO V^T (Q and dO
 // staged row-major in LDS as A operands), then dV^T += dO^T P and dK^T += Q^T dS (Q^T and dO^T
 // staged transposed, P and dS from registers in the permuted query order). Each key's dK and
-// dV are summed by one lane in a fixed order over heads and query tiles, so the result is
-// bitwise reproducible. Runs after k_attn_bwd_dq (it reads delta).
+// dV are summed by one lane in a fixed order over heads and query tiles; with the heads split
+// over several blocks (short inputs, to fill the GPU), each part writes fp32 partials and
+// k_attn_dkdv_reduce adds them in part order, so the result is bitwise reproducible. Runs after
+// k_attn_bwd_dq (it reads delta).
 #include <cmath>
 
 #include "attention.hpp"
@@ -124,6 +127,49 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_bwd_dq(const AttnBwdArgs 
                      a.scale);
 }
 
+// A [ROWS x D] tile prefetched into registers in row pairs: thread tid takes pairs
+// idx = tid + 256 j, rows (2p, 2p + 1) of 8-column chunk dc (p = idx % (ROWS / 2),
+// dc = idx / (ROWS / 2)); store() writes it to LDS row-major (pitch RP) and transposed (pitch
+// CP) in one go, so each global chunk is read once for both copies.
+template <typename T, int D, int ROWS>
+struct TilePairs {
+  static constexpr int N = (ROWS / 2) * (D / 8) / kAttnThreads;
+  static_assert(N >= 1 && (ROWS / 2) * (D / 8) % kAttnThreads == 0, "tile / block mismatch");
+  uint4 r0[N], r1[N];
+
+  __device__ __forceinline__ void load(const T* base, int64_t rs, int t0, int tend, int tid) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = tid + kAttnThreads * j;
+      const int p = idx % (ROWS / 2), dc = idx / (ROWS / 2);
+      const int t = t0 + 2 * p;
+      r0[j] = t < tend ? *reinterpret_cast<const uint4*>(base + (int64_t)t * rs + 8 * dc)
+                       : make_uint4(0, 0, 0, 0);
+      r1[j] = t + 1 < tend ? *reinterpret_cast<const uint4*>(base + (int64_t)(t + 1) * rs + 8 * dc)
+                           : make_uint4(0, 0, 0, 0);
+    }
+  }
+
+  template <int RP, int CP>
+  __device__ __forceinline__ void store(T* rows, T* cols, int tid) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = tid + kAttnThreads * j;
+      const int p = idx % (ROWS / 2), dc = idx / (ROWS / 2);
+      *reinterpret_cast<uint4*>(&rows[(2 * p) * RP + 8 * dc]) = r0[j];
+      *reinterpret_cast<uint4*>(&rows[(2 * p + 1) * RP + 8 * dc]) = r1[j];
+      const uint32_t w0[4] = {r0[j].x, r0[j].y, r0[j].z, r0[j].w};
+      const uint32_t w1[4] = {r1[j].x, r1[j].y, r1[j].z, r1[j].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t lo = (w0[e / 2] >> (16 * (e % 2))) & 0xffffu;
+        const uint32_t up = (w1[e / 2] >> (16 * (e % 2))) & 0xffffu;
+        *reinterpret_cast<uint32_t*>(&cols[(8 * dc + e) * CP + 2 * p]) = lo | (up << 16);
+      }
+    }
+  }
+};
+
 template <typename T, int D>
 __global__ __launch_bounds__(kAttnThreads) void k_attn_bwd_dkdv(const AttnBwdArgs b) {
   using V8 = typename Mfma<T>::v8;
@@ -137,7 +183,9 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_bwd_dkdv(const AttnBwdArg
   __shared__ __align__(16) T dt_[D * CP];   // dO^T (A operand of dV^T)
   __shared__ float lse_s[BQ], del_s[BQ];
 
-  const int seq = blockIdx.z, kh = blockIdx.y;
+  const int seq = blockIdx.z;
+  const int split = b.split;                 // query-head groups per kv head
+  const int kh = blockIdx.y / split, part = blockIdx.y % split;
   int start, end;
   seq_bounds(a.cu, seq, a.T, &start, &end);
   const int ntiles = (end - start + kAttnBK - 1) / kAttnBK;
@@ -149,7 +197,8 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_bwd_dkdv(const AttnBwdArg
   const int kj = kw0 + lq;      // this lane's key
   const bool kok = kj < end;
   const bool wave_live = kw0 < end;
-  const int G = a.HQ / a.HK;
+  const int gs = a.HQ / a.HK / split;          // query heads of this block
+  const int h0 = kh * (a.HQ / a.HK) + part * gs;
 
   // K and V of this lane's key as B operands (B[d][key] = K[key][d]).
   V8 kb[D / 16], vb[D / 16];
@@ -167,67 +216,121 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_bwd_dkdv(const AttnBwdArg
 #pragma unroll
   for (int md = 0; md < D / 32; ++md) dka[md] = dva[md] = f32x16{};
 
-  for (int g = 0; g < G; ++g) {
-    const int h = kh * G + g;
-    const T* qbase = static_cast<const T*>(a.q) + (int64_t)h * D;
-    const T* dbase = static_cast<const T*>(b.dout) + (int64_t)h * D;
-    for (int qt = k0; qt < end; qt += BQ) {
-      __syncthreads();
-      stage_rows<T, D, BQ, RP>(qs, qbase, a.q_rs, qt, end, tid);
-      stage_rows<T, D, BQ, RP>(ds_, dbase, b.do_rs, qt, end, tid);
-      stage_cols<T, D, BQ, CP>(qt_, qbase, a.q_rs, qt, end, tid);
-      stage_cols<T, D, BQ, CP>(dt_, dbase, b.do_rs, qt, end, tid);
-      if (tid < BQ) {
-        const int t = qt + tid;
-        lse_s[tid] = t < end ? a.lse[(int64_t)h * a.T + t] * kLog2e : 0.f;
-        del_s[tid] = t < end ? b.delta[(int64_t)h * a.T + t] : 0.f;
-      }
-      __syncthreads();
-      // every query of the tile comes before this wave's keys: nothing to add
-      if (!wave_live || qt + BQ - 1 < kw0) continue;
+  // Work items (head, query tile) in order; the next item's Q, dO, lse and delta are loaded
+  // into registers while the current one is computed.
+  const int nqt = (end - k0 + BQ - 1) / BQ;
+  const int items = gs * nqt;
+  TilePairs<T, D, BQ> pq, pd;
+  float lse_n = 0.f, del_n = 0.f;
+  auto prefetch = [&](int it) {
+    const int h = h0 + it / nqt, qt = k0 + (it % nqt) * BQ;
+    const int64_t col = (int64_t)h * D;
+    pq.load(static_cast<const T*>(a.q) + col, a.q_rs, qt, end, tid);
+    pd.load(static_cast<const T*>(b.dout) + col, b.do_rs, qt, end, tid);
+    if (tid < BQ) {
+      const int t = qt + tid;
+      lse_n = t < end ? a.lse[(int64_t)h * a.T + t] * kLog2e : 0.f;
+      del_n = t < end ? b.delta[(int64_t)h * a.T + t] : 0.f;
+    }
+  };
+  if (items > 0) prefetch(0);
 
-      V8 pb[2][2], sb_[2][2];
+  for (int it = 0; it < items; ++it) {
+    const int qt = k0 + (it % nqt) * BQ;
+    __syncthreads();  // the previous item's LDS reads are done
+    pq.template store<RP, CP>(qs, qt_, tid);
+    pd.template store<RP, CP>(ds_, dt_, tid);
+    if (tid < BQ) {
+      lse_s[tid] = lse_n;
+      del_s[tid] = del_n;
+    }
+    __syncthreads();
+    if (it + 1 < items) prefetch(it + 1);
+    // every query of the tile comes before this wave's keys: nothing to add
+    if (!wave_live || qt + BQ - 1 < kw0) continue;
+
+    V8 pb[2][2], sb_[2][2];
 #pragma unroll
-      for (int qh = 0; qh < 2; ++qh) {
-        f32x16 s = f32x16{}, dp = f32x16{};
-        const T* qrow = &qs[(32 * qh + lq) * RP + 8 * hi];
-        const T* drow = &ds_[(32 * qh + lq) * RP + 8 * hi];
+    for (int qh = 0; qh < 2; ++qh) {
+      f32x16 s = f32x16{}, dp = f32x16{};
+      const T* qrow = &qs[(32 * qh + lq) * RP + 8 * hi];
+      const T* drow = &ds_[(32 * qh + lq) * RP + 8 * hi];
 #pragma unroll
-        for (int c = 0; c < D / 16; ++c) {
-          s = Mfma<T>::run(ld16<V8>(qrow + 16 * c), kb[c], s);
-          dp = Mfma<T>::run(ld16<V8>(drow + 16 * c), vb[c], dp);
-        }
-        // s[i] is S[q][kj] for query row r = 32 qh + 8 (i / 4) + 4 hi + i % 4 of the tile
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int r = 32 * qh + 8 * (i / 4) + 4 * hi + (i % 4);
-          const int t = qt + r;
-          const float p = (kj <= t && t < end) ? exp2f(s[i] * a.scale_log2 - lse_s[r]) : 0.f;
-          pb[qh][i / 8][i % 8] = (T)p;
-          sb_[qh][i / 8][i % 8] = (T)(p * (dp[i] - del_s[r]));
-        }
+      for (int c = 0; c < D / 16; ++c) {
+        s = Mfma<T>::run(ld16<V8>(qrow + 16 * c), kb[c], s);
+        dp = Mfma<T>::run(ld16<V8>(drow + 16 * c), vb[c], dp);
       }
-      // dV^T += dO^T P and dK^T += Q^T dS, queries in the permuted order of pb / sb_
+      // s[i] is S[q][kj] for query row r = 32 qh + 8 (i / 4) + 4 hi + i % 4 of the tile
 #pragma unroll
-      for (int md = 0; md < D / 32; ++md) {
-        const T* drow = &dt_[(32 * md + lq) * CP + 4 * hi];
-        const T* qrow = &qt_[(32 * md + lq) * CP + 4 * hi];
-#pragma unroll
-        for (int qh = 0; qh < 2; ++qh)
-#pragma unroll
-          for (int c2 = 0; c2 < 2; ++c2) {
-            const int rb = 32 * qh + 16 * c2;
-            dva[md] = Mfma<T>::run(ld8x2<V8>(drow + rb, drow + rb + 8), pb[qh][c2], dva[md]);
-            dka[md] = Mfma<T>::run(ld8x2<V8>(qrow + rb, qrow + rb + 8), sb_[qh][c2], dka[md]);
-          }
+      for (int i = 0; i < 16; ++i) {
+        const int r = 32 * qh + 8 * (i / 4) + 4 * hi + (i % 4);
+        const int t = qt + r;
+        const float p = (kj <= t && t < end) ? exp2f(s[i] * a.scale_log2 - lse_s[r]) : 0.f;
+        pb[qh][i / 8][i % 8] = (T)p;
+        sb_[qh][i / 8][i % 8] = (T)(p * (dp[i] - del_s[r]));
       }
+    }
+    // dV^T += dO^T P and dK^T += Q^T dS, queries in the permuted order of pb / sb_
+#pragma unroll
+    for (int md = 0; md < D / 32; ++md) {
+      const T* drow = &dt_[(32 * md + lq) * CP + 4 * hi];
+      const T* qrow = &qt_[(32 * md + lq) * CP + 4 * hi];
+#pragma unroll
+      for (int qh = 0; qh < 2; ++qh)
+#pragma unroll
+        for (int c2 = 0; c2 < 2; ++c2) {
+          const int rb = 32 * qh + 16 * c2;
+          dva[md] = Mfma<T>::run(ld8x2<V8>(drow + rb, drow + rb + 8), pb[qh][c2], dva[md]);
+          dka[md] = Mfma<T>::run(ld8x2<V8>(qrow + rb, qrow + rb + 8), sb_[qh][c2], dka[md]);
+        }
     }
   }
   if (!kok) return;
-  store_rows_t<T, D>(static_cast<T*>(b.dk) + (int64_t)kj * b.dk_rs + (int64_t)kh * D, dka, hi,
-                     a.scale);
-  store_rows_t<T, D>(static_cast<T*>(b.dv) + (int64_t)kj * b.dv_rs + (int64_t)kh * D, dva, hi,
-                     1.f);
+  if (split == 1) {
+    store_rows_t<T, D>(static_cast<T*>(b.dk) + (int64_t)kj * b.dk_rs + (int64_t)kh * D, dka, hi,
+                       a.scale);
+    store_rows_t<T, D>(static_cast<T*>(b.dv) + (int64_t)kj * b.dv_rs + (int64_t)kh * D, dva, hi,
+                       1.f);
+    return;
+  }
+  // fp32 partials [split][T][HK][D] of dK^T / scale and dV^T, summed by k_attn_dkdv_reduce
+  const int64_t plane = a.T * a.HK * D;
+  float* pk = b.part + (int64_t)part * plane + ((int64_t)kj * a.HK + kh) * D + 4 * hi;
+  float* pv = pk + (int64_t)split * plane;
+#pragma unroll
+  for (int md = 0; md < D / 32; ++md)
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      *reinterpret_cast<float4*>(pk + 32 * md + 8 * j) =
+          make_float4(dka[md][4 * j], dka[md][4 * j + 1], dka[md][4 * j + 2], dka[md][4 * j + 3]);
+      *reinterpret_cast<float4*>(pv + 32 * md + 8 * j) =
+          make_float4(dva[md][4 * j], dva[md][4 * j + 1], dva[md][4 * j + 2], dva[md][4 * j + 3]);
+    }
+}
+
+// dK = scale * sum_s dK_s, dV = sum_s dV_s over the split partials, s ascending. One thread per
+// 4 consecutive elements of a [T, HK, D] plane.
+template <typename T>
+__global__ __launch_bounds__(256) void k_attn_dkdv_reduce(const AttnBwdArgs b, int D) {
+  const int64_t plane = b.f.T * b.f.HK * D;
+  const int64_t e = 4 * ((int64_t)blockIdx.x * blockDim.x + threadIdx.x);
+  if (e >= plane) return;
+  const int64_t t = e / ((int64_t)b.f.HK * D), r = e % ((int64_t)b.f.HK * D);
+  for (int which = 0; which < 2; ++which) {
+    const float* src = b.part + (int64_t)which * b.split * plane + e;
+    float4 acc = *reinterpret_cast<const float4*>(src);
+    for (int s = 1; s < b.split; ++s) {
+      const float4 v = *reinterpret_cast<const float4*>(src + (int64_t)s * plane);
+      acc.x += v.x;
+      acc.y += v.y;
+      acc.z += v.z;
+      acc.w += v.w;
+    }
+    const float mul = which == 0 ? b.f.scale : 1.f;
+    T o4[4] = {(T)(acc.x * mul), (T)(acc.y * mul), (T)(acc.z * mul), (T)(acc.w * mul)};
+    T* dst = static_cast<T*>(which == 0 ? b.dk : b.dv) + t * (which == 0 ? b.dk_rs : b.dv_rs) + r;
+    *reinterpret_cast<uint2*>(dst) = __builtin_bit_cast(uint2, o4);
+  }
 }
 
 template <typename T, int D>
@@ -236,8 +339,13 @@ hipError_t bwd_run(const AttnBwdArgs& b, int max_seqlen, hipStream_t s) {
   hipLaunchKernelGGL((k_attn_bwd_dq<T, D>), gq, dim3(kAttnThreads), 0, s, b);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const dim3 gk((max_seqlen + kAttnBK - 1) / kAttnBK, b.f.HK, b.f.n_seq);
+  const dim3 gk((max_seqlen + kAttnBK - 1) / kAttnBK, b.f.HK * b.split, b.f.n_seq);
   hipLaunchKernelGGL((k_attn_bwd_dkdv<T, D>), gk, dim3(kAttnThreads), 0, s, b);
+  e = hipGetLastError();
+  if (e != hipSuccess || b.split == 1) return e;
+  const int64_t quads = b.f.T * b.f.HK * D / 4;
+  hipLaunchKernelGGL((k_attn_dkdv_reduce<T>), dim3((unsigned)((quads + 255) / 256)), dim3(256), 0,
+                     s, b, D);
   return hipGetLastError();
 }
 

@@ -70,6 +70,20 @@ int64_t bwd_partials(int64_t rows, int64_t n) {
   return p < 1 ? 1 : p;
 }
 
+// Blocks per (kv head, key tile) of the attention dK / dV kernel: split the kv head's query
+// heads over more blocks (the smallest divisor of HQ / HK that gives >= 512 blocks for T tokens),
+// each writing fp32 partials, when one block per kv head would leave the GPU half empty.
+int attn_split(int64_t T, int HQ, int HK) {
+  const int G = HQ / HK;
+  const int64_t blocks = ((T + esep::kAttnBK - 1) / esep::kAttnBK) * HK;
+  int s = 1;
+  while (blocks * s < 512 && s < G) {
+    ++s;
+    while (G % s) ++s;
+  }
+  return s;
+}
+
 }  // namespace
 
 extern "C" {
@@ -397,9 +411,16 @@ int esep_attn_fwd(const void* q, int64_t q_rs, const void* k, int64_t k_rs, cons
   return e == hipSuccess ? 0 : hip_fail(e, "attn_fwd launch");
 }
 
+int64_t esep_attn_bwd_workspace(int64_t T, int HQ, int HK, int D) {
+  if (T <= 0 || HQ < 1 || HK < 1 || HQ % HK != 0 || D < 1) return 0;
+  const int s = attn_split(T, HQ, HK);
+  const int64_t delta = ((int64_t)HQ * T + 3) & ~(int64_t)3;  // keeps the partials 16-byte aligned
+  return delta + (s > 1 ? 2 * (int64_t)s * T * HK * D : 0);
+}
+
 int esep_attn_bwd(const void* q, int64_t q_rs, const void* k, int64_t k_rs, const void* v,
                   int64_t v_rs, const void* o, int64_t o_rs, const void* dout, int64_t do_rs,
-                  const float* lse, float* delta, void* dq, int64_t dq_rs, void* dk,
+                  const float* lse, float* workspace, void* dq, int64_t dq_rs, void* dk,
                   int64_t dk_rs, void* dv, int64_t dv_rs, int dt, int64_t T, int HQ, int HK,
                   int D, const int32_t* cu_seqlens, int n_seq, int max_seqlen, float scale,
                   void* stream) {
@@ -418,8 +439,9 @@ int esep_attn_bwd(const void* q, int64_t q_rs, const void* k, int64_t k_rs, cons
   const void* ptrs[] = {q, k, v, o, dout, dq, dk, dv};
   for (const void* p : ptrs)
     if (p == nullptr) return fail(ESEP_EINVAL, "attn_bwd: q, k, v, o, dout, dq, dk, dv are required");
-  if (lse == nullptr || delta == nullptr || cu_seqlens == nullptr)
-    return fail(ESEP_EINVAL, "attn_bwd: lse, the delta workspace and cu_seqlens are required");
+  if (lse == nullptr || workspace == nullptr || cu_seqlens == nullptr)
+    return fail(ESEP_EINVAL, "attn_bwd: lse, the workspace and cu_seqlens are required");
+  if (!aligned16(workspace)) return fail(ESEP_EALIGN, "attn_bwd: workspace needs 16-byte alignment");
   const int64_t rss[] = {q_rs, k_rs, v_rs, o_rs, do_rs, dq_rs, dk_rs, dv_rs};
   for (int i = 0; i < 8; ++i)
     if (!aligned16(ptrs[i]) || (rss[i] & 7))
@@ -444,7 +466,9 @@ int esep_attn_bwd(const void* q, int64_t q_rs, const void* k, int64_t k_rs, cons
   b.f.scale = scale;
   b.f.scale_log2 = scale * 1.4426950408889634f;
   b.dout = dout;
-  b.delta = delta;
+  b.delta = workspace;
+  b.split = attn_split(T, HQ, HK);
+  b.part = workspace + (((int64_t)HQ * T + 3) & ~(int64_t)3);
   b.dq = dq;
   b.dk = dk;
   b.dv = dv;

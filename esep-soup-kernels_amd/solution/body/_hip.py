@@ -44,6 +44,7 @@ SIGNATURES = {
     "esep_dgamma_reduce": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp]),
     "esep_attn_fwd": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i32, _i64, _i32,
                              _i32, _i32, _vp, _i32, _i32, _f32, _vp]),
+    "esep_attn_bwd_workspace": (_i64, [_i64, _i32, _i32, _i32]),
     "esep_attn_bwd": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp,
                              _vp, _i64, _vp, _i64, _vp, _i64, _i32, _i64, _i32, _i32, _i32, _vp,
                              _i32, _i32, _f32, _vp]),
@@ -316,11 +317,17 @@ def attn_fwd(q, k, v, o, cu_seqlens, max_seqlen, scale, lse=None, name="_attn_fw
     _record(name)
 
 
-def attn_bwd(q, k, v, o, dout, lse, dq, dk, dv, cu_seqlens, max_seqlen, scale, delta=None,
+def attn_bwd_workspace(T, HQ, HK, D):
+    """Floats of fp32 workspace esep_attn_bwd needs for this shape."""
+    return int(lib().esep_attn_bwd_workspace(int(T), int(HQ), int(HK), int(D)))
+
+
+def attn_bwd(q, k, v, o, dout, lse, dq, dk, dv, cu_seqlens, max_seqlen, scale, workspace=None,
              name="_attn_bwd"):
-    """Backward of attn_fwd (esep_attn_bwd): dq [T, HQ, D], dk, dv [T, HK, D] out. `delta` is
-    the fp32 [HQ, T] workspace (allocated here when not given)."""
-    dev = _dev(q, k, v, o, dout, lse, dq, dk, dv, cu_seqlens, delta)
+    """Backward of attn_fwd (esep_attn_bwd): dq [T, HQ, D], dk, dv [T, HK, D] out. `workspace`
+    is a contiguous fp32 tensor of >= attn_bwd_workspace(T, HQ, HK, D) elements (allocated here
+    when not given)."""
+    dev = _dev(q, k, v, o, dout, lse, dq, dk, dv, cu_seqlens, workspace)
     T, HQ, D = q.shape
     HK = k.shape[1]
     for t, shp in ((o, (T, HQ, D)), (dout, (T, HQ, D)), (dq, (T, HQ, D)), (k, (T, HK, D)),
@@ -331,13 +338,15 @@ def attn_bwd(q, k, v, o, dout, lse, dq, dk, dv, cu_seqlens, max_seqlen, scale, d
         raise EsepError("lse must be a contiguous fp32 [HQ, T] tensor")
     if cu_seqlens.dtype != torch.int32 or not cu_seqlens.is_contiguous():
         raise EsepError("cu_seqlens must be a contiguous int32 tensor")
-    if delta is None:
-        delta = torch.empty((HQ, T), device=dev, dtype=torch.float32)
-    elif delta.dtype != torch.float32 or not delta.is_contiguous() or tuple(delta.shape) != (HQ, T):
-        raise EsepError("delta must be a contiguous fp32 [HQ, T] tensor")
+    need = attn_bwd_workspace(T, HQ, HK, D)
+    if workspace is None:
+        workspace = torch.empty(max(need, 1), device=dev, dtype=torch.float32)
+    elif (workspace.dtype != torch.float32 or not workspace.is_contiguous()
+          or workspace.numel() < need or workspace.device != dev):
+        raise EsepError(f"workspace must be a contiguous fp32 tensor of >= {need} elements")
     rc = lib().esep_attn_bwd(
         _p(q), _tokens_ld(q, "q"), _p(k), _tokens_ld(k, "k"), _p(v), _tokens_ld(v, "v"),
-        _p(o), _tokens_ld(o, "o"), _p(dout), _tokens_ld(dout, "dout"), _p(lse), _p(delta),
+        _p(o), _tokens_ld(o, "o"), _p(dout), _tokens_ld(dout, "dout"), _p(lse), _p(workspace),
         _p(dq), _tokens_ld(dq, "dq"), _p(dk), _tokens_ld(dk, "dk"), _p(dv), _tokens_ld(dv, "dv"),
         dtype_code(q.dtype), T, HQ, HK, D, _p(cu_seqlens), cu_seqlens.numel() - 1,
         int(max_seqlen), float(scale), _stream(dev))

@@ -191,19 +191,27 @@ int esep_attn_fwd(const void* q, int64_t q_rs, const void* k, int64_t k_rs, cons
                   float scale, void* stream);
 
 /*
+ * Floats of fp32 workspace that esep_attn_bwd needs for this shape (depends on the shape only).
+ * No reference counterpart (the reference's SDPA allocates inside torch).
+ */
+int64_t esep_attn_bwd_workspace(int64_t T, int HQ, int HK, int D);
+
+/*
  * Backward of esep_attn_fwd (same layout and argument meanings), deterministic (no atomics).
  * Replaces the autograd backward of the reference's per-row SDPA calls (packed.py:428-429).
  *
  *   o, lse    the forward's output and its saved lse
  *   dout      [T, HQ, D] gradient of o
- *   delta     fp32 [HQ, T] workspace (caller-allocated; rowsum(dout * o), written then read)
+ *   workspace fp32, esep_attn_bwd_workspace(T, HQ, HK, D) floats, 16-byte aligned, caller-
+ *             allocated (per-query rowsum(dout * o), then dK / dV partials when the query heads
+ *             of a kv head are spread over several blocks to fill the GPU; written then read)
  *   dq [T, HQ, D], dk, dv [T, HK, D]   outputs in dt; dk and dv sum over the query heads of
  *                                      their group in a fixed order
  * Two kernels on the stream: dQ (and delta) per query tile, then dK and dV per key tile.
  */
 int esep_attn_bwd(const void* q, int64_t q_rs, const void* k, int64_t k_rs, const void* v,
                   int64_t v_rs, const void* o, int64_t o_rs, const void* dout, int64_t do_rs,
-                  const float* lse, float* delta, void* dq, int64_t dq_rs, void* dk,
+                  const float* lse, float* workspace, void* dq, int64_t dq_rs, void* dk,
                   int64_t dk_rs, void* dv, int64_t dv_rs, int dt, int64_t T, int HQ, int HK,
                   int D, const int32_t* cu_seqlens, int n_seq, int max_seqlen, float scale,
                   void* stream);
