@@ -10,11 +10,11 @@
 //
 // Forward mapping (flash-attention style, one pass, online softmax). A block of 4 wavefronts
 // owns 128 queries of one sequence and one query head; wavefront w owns queries 32w..32w+31 of
-// the block. Keys are walked in tiles of 64 (the tiles the causal mask leaves), heaviest query
-// tiles first. Scores are computed transposed, S^T = K Q^T, with v_mfma_f32_32x32x16 (K from
-// LDS as the A operand, the wave's Q held in registers as the B operand), so each lane owns one
-// query and 32 of a tile's 64 scores; the other 32 sit in lane l ^ 32, and a row max or sum is
-// a register reduction plus one cross-half exchange. The probabilities go straight from the
+// the block. Keys are staged in tiles of 64 (the tiles the causal mask leaves) and consumed in
+// halves of 32, heaviest query tiles first. Scores are computed transposed, S^T = K Q^T, with
+// v_mfma_f32_32x32x16 (K from LDS as the A operand, the wave's Q held in registers as the B
+// operand), so each lane owns one query and 16 of a half's 32 scores; the other 16 sit in lane
+// l ^ 32, and a row max or sum is a register reduction plus one cross-half exchange. The probabilities go straight from the
 // score registers into O^T += V^T P^T: the contraction over keys is permuted so that the B
 // operand a lane needs is exactly the scores it holds, and V^T (staged transposed in LDS) is
 // read in the same permuted key order.

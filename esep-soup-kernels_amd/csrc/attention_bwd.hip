@@ -30,7 +30,8 @@ namespace {
 constexpr float kLog2e = 1.4426950408889634f;
 
 template <typename T, int D>
-__global__ __launch_bounds__(kAttnThreads) void k_attn_bwd_dq(const AttnBwdArgs b) {
+// 2 wavefronts per SIMD without spills (unbounded, the compiler settles at 1).
+__global__ __launch_bounds__(kAttnThreads, 2) void k_attn_bwd_dq(const AttnBwdArgs b) {
   using V8 = typename Mfma<T>::v8;
   const AttnArgs& a = b.f;
   constexpr int BN = kAttnBN;
@@ -91,7 +92,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_bwd_dq(const AttnBwdArgs 
     __syncthreads();
     if (!wave_live || kt > wq_last) continue;
 
-    V8 dsb[2][2];
+    // one 32-key half at a time (fewer live registers: 3 wavefronts per SIMD instead of 2)
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
       f32x16 s = f32x16{}, dp = f32x16{};
@@ -102,24 +103,23 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_bwd_dq(const AttnBwdArgs 
         s = Mfma<T>::run(ld16<V8>(krow + 16 * c), qb[c], s);
         dp = Mfma<T>::run(ld16<V8>(vrow + 16 * c), db[c], dp);
       }
+      V8 dsb[2];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int kj = kt + 32 * sb + 8 * (i / 4) + 4 * hi + (i % 4);
         const float p = kj <= qi ? exp2f(s[i] * a.scale_log2 - lse2) : 0.f;
-        dsb[sb][i / 8][i % 8] = (T)(p * (dp[i] - delta));
+        dsb[i / 8][i % 8] = (T)(p * (dp[i] - delta));
       }
-    }
-    // dQ^T += K^T dS^T, keys in the permuted order of dsb
+      // dQ^T += K^T dS^T, keys in the permuted order of dsb
 #pragma unroll
-    for (int md = 0; md < D / 32; ++md) {
-      const T* trow = &kt_[(32 * md + lq) * TP + 4 * hi];
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb)
+      for (int md = 0; md < D / 32; ++md) {
+        const T* trow = &kt_[(32 * md + lq) * TP + 4 * hi];
 #pragma unroll
         for (int c2 = 0; c2 < 2; ++c2) {
           const int kb = 32 * sb + 16 * c2;
-          dqa[md] = Mfma<T>::run(ld8x2<V8>(trow + kb, trow + kb + 8), dsb[sb][c2], dqa[md]);
+          dqa[md] = Mfma<T>::run(ld8x2<V8>(trow + kb, trow + kb + 8), dsb[c2], dqa[md]);
         }
+      }
     }
   }
   if (!qok) return;
@@ -249,7 +249,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_bwd_dkdv(const AttnBwdArg
     // every query of the tile comes before this wave's keys: nothing to add
     if (!wave_live || qt + BQ - 1 < kw0) continue;
 
-    V8 pb[2][2], sb_[2][2];
+    // one 32-query half at a time
 #pragma unroll
     for (int qh = 0; qh < 2; ++qh) {
       f32x16 s = f32x16{}, dp = f32x16{};
@@ -261,28 +261,27 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_bwd_dkdv(const AttnBwdArg
         dp = Mfma<T>::run(ld16<V8>(drow + 16 * c), vb[c], dp);
       }
       // s[i] is S[q][kj] for query row r = 32 qh + 8 (i / 4) + 4 hi + i % 4 of the tile
+      V8 pb[2], sb_[2];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int r = 32 * qh + 8 * (i / 4) + 4 * hi + (i % 4);
         const int t = qt + r;
         const float p = (kj <= t && t < end) ? exp2f(s[i] * a.scale_log2 - lse_s[r]) : 0.f;
-        pb[qh][i / 8][i % 8] = (T)p;
-        sb_[qh][i / 8][i % 8] = (T)(p * (dp[i] - del_s[r]));
+        pb[i / 8][i % 8] = (T)p;
+        sb_[i / 8][i % 8] = (T)(p * (dp[i] - del_s[r]));
       }
-    }
-    // dV^T += dO^T P and dK^T += Q^T dS, queries in the permuted order of pb / sb_
+      // dV^T += dO^T P and dK^T += Q^T dS, queries in the permuted order of pb / sb_
 #pragma unroll
-    for (int md = 0; md < D / 32; ++md) {
-      const T* drow = &dt_[(32 * md + lq) * CP + 4 * hi];
-      const T* qrow = &qt_[(32 * md + lq) * CP + 4 * hi];
-#pragma unroll
-      for (int qh = 0; qh < 2; ++qh)
+      for (int md = 0; md < D / 32; ++md) {
+        const T* dtr = &dt_[(32 * md + lq) * CP + 4 * hi];
+        const T* qtr = &qt_[(32 * md + lq) * CP + 4 * hi];
 #pragma unroll
         for (int c2 = 0; c2 < 2; ++c2) {
           const int rb = 32 * qh + 16 * c2;
-          dva[md] = Mfma<T>::run(ld8x2<V8>(drow + rb, drow + rb + 8), pb[qh][c2], dva[md]);
-          dka[md] = Mfma<T>::run(ld8x2<V8>(qrow + rb, qrow + rb + 8), sb_[qh][c2], dka[md]);
+          dva[md] = Mfma<T>::run(ld8x2<V8>(dtr + rb, dtr + rb + 8), pb[c2], dva[md]);
+          dka[md] = Mfma<T>::run(ld8x2<V8>(qtr + rb, qtr + rb + 8), sb_[c2], dka[md]);
         }
+      }
     }
   }
   if (!kok) return;

@@ -7,7 +7,9 @@ namespace esep {
 namespace {
 
 template <typename T, int D>
-__global__ __launch_bounds__(kAttnThreads) void k_attn_fwd(const AttnArgs a) {
+// 3 wavefronts per SIMD (<= 168 registers): without the bound the compiler parks the
+// accumulators in AGPRs and stops at 2.
+__global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd(const AttnArgs a) {
   using V8 = typename Mfma<T>::v8;
   constexpr int BN = kAttnBN;
   constexpr int KP = D + 8;   // K row pitch in LDS (elements): rows land on different banks
@@ -53,57 +55,52 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_fwd(const AttnArgs a) {
     __syncthreads();
     if (!wave_live || kt > wq_last) continue;  // every key of the tile is after this wave's queries
 
-    // S^T = K Q^T for the two 32-key halves of the tile; lane (lq, hi) gets the scores of query
+    // One 32-key half at a time: scores, online-softmax update, then P V for that half.
+    // (Keeping both halves' scores live needs ~250 registers, 2 wavefronts per SIMD; one half
+    // at a time fits 3, which measured a third faster.) Lane (lq, hi) gets the scores of query
     // qi against keys kt + 32 sb + 8 (i / 4) + 4 hi + i % 4, i < 16.
-    float sc[2][16];
 #pragma unroll
     for (int sb = 0; sb < 2; ++sb) {
       f32x16 acc = f32x16{};
       const T* krow = &ks[(32 * sb + lq) * KP + 8 * hi];
 #pragma unroll
       for (int c = 0; c < D / 16; ++c) acc = Mfma<T>::run(ld16<V8>(krow + 16 * c), qb[c], acc);
+      float sc[16];
+      float mx = -INFINITY;
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
         const int kj = kt + 32 * sb + 8 * (i / 4) + 4 * hi + (i % 4);
-        sc[sb][i] = kj <= qi ? acc[i] * a.scale_log2 : -INFINITY;
+        sc[i] = kj <= qi ? acc[i] * a.scale_log2 : -INFINITY;
+        mx = fmaxf(mx, sc[i]);
       }
-    }
-    // online softmax (base 2): running max m and sum l per query
-    float mx = -INFINITY;
-#pragma unroll
-    for (int sb = 0; sb < 2; ++sb)
-#pragma unroll
-      for (int i = 0; i < 16; ++i) mx = fmaxf(mx, sc[sb][i]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float mnew = fmaxf(m, mx);
-    const float mu = mnew == -INFINITY ? 0.f : mnew;
-    const float alpha = exp2f(m - mu);
-    float ps = 0.f;
-    V8 pb[2][2];
-#pragma unroll
-    for (int sb = 0; sb < 2; ++sb)
+      // online softmax (base 2): running max m and sum l per query
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      const float mnew = fmaxf(m, mx);
+      const float mu = mnew == -INFINITY ? 0.f : mnew;
+      const float alpha = exp2f(m - mu);
+      float ps = 0.f;
+      V8 pb[2];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float p = exp2f(sc[sb][i] - mu);
+        const float p = exp2f(sc[i] - mu);
         ps += p;
-        pb[sb][i / 8][i % 8] = (T)p;
+        pb[i / 8][i % 8] = (T)p;
       }
-    ps += __shfl_xor(ps, 32);
-    l = l * alpha + ps;
-    m = mnew;
-    // O^T += V^T P^T over the 64 keys, contraction in the permuted key order of pb: element e
-    // of chunk (sb, c2) is key 32 sb + 16 c2 + 8 (e / 4) + 4 hi + e % 4.
+      ps += __shfl_xor(ps, 32);
+      l = l * alpha + ps;
+      m = mnew;
+      // O^T += V^T P^T over the 32 keys, contraction in the permuted key order of pb: element e
+      // of chunk c2 is key 32 sb + 16 c2 + 8 (e / 4) + 4 hi + e % 4.
 #pragma unroll
-    for (int md = 0; md < D / 32; ++md) {
-      oacc[md] *= alpha;
-      const T* vrow = &vt[(32 * md + lq) * VP + 4 * hi];
-#pragma unroll
-      for (int sb = 0; sb < 2; ++sb)
+      for (int md = 0; md < D / 32; ++md) {
+        oacc[md] *= alpha;
+        const T* vrow = &vt[(32 * md + lq) * VP + 4 * hi];
 #pragma unroll
         for (int c2 = 0; c2 < 2; ++c2) {
           const int kb = 32 * sb + 16 * c2;
-          oacc[md] = Mfma<T>::run(ld8x2<V8>(vrow + kb, vrow + kb + 8), pb[sb][c2], oacc[md]);
+          oacc[md] = Mfma<T>::run(ld8x2<V8>(vrow + kb, vrow + kb + 8), pb[c2], oacc[md]);
         }
+      }
     }
   }
 
