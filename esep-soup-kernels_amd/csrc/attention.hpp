@@ -64,7 +64,6 @@ struct AttnBwdArgs {
 constexpr int kAttnBM = 128;  // queries per forward / dQ block (4 wavefronts x 32)
 constexpr int kAttnBN = 64;   // keys per tile
 constexpr int kAttnThreads = 256;
-constexpr int kAttnBK = 128;  // keys per dK / dV block (4 wavefronts x 32)
 constexpr int kAttnBQ = 64;   // queries per dK / dV tile
 
 hipError_t launch_attn_fwd(const AttnArgs& a, int dt, int D, int max_seqlen, hipStream_t s,
@@ -118,10 +117,10 @@ __device__ __forceinline__ void seq_bounds(const int32_t* cu, int s, int64_t T, 
 
 // Stage a [rows x D] tile (token rows r0 .. r0 + rows - 1 below rend; the rest reads as 0)
 // into LDS row-major with pitch P elements.
-template <typename T, int D, int ROWS, int P>
+template <typename T, int D, int ROWS, int P, int NT = kAttnThreads>
 __device__ __forceinline__ void stage_rows(T* dst, const T* base, int64_t rs, int r0, int rend,
                                            int tid) {
-  for (int idx = tid; idx < ROWS * (D / 8); idx += kAttnThreads) {
+  for (int idx = tid; idx < ROWS * (D / 8); idx += NT) {
     const int r = idx % ROWS, dc = idx / ROWS;
     uint4 val = make_uint4(0, 0, 0, 0);
     if (r0 + r < rend) val = *reinterpret_cast<const uint4*>(base + (int64_t)(r0 + r) * rs + 8 * dc);
@@ -131,10 +130,10 @@ __device__ __forceinline__ void stage_rows(T* dst, const T* base, int64_t rs, in
 
 // Stage the same tile transposed, [D x ROWS] with pitch P: a thread takes rows (2p, 2p + 1) of
 // one 8-column chunk and writes 8 dwords (one per column), each holding the two rows' values.
-template <typename T, int D, int ROWS, int P>
+template <typename T, int D, int ROWS, int P, int NT = kAttnThreads>
 __device__ __forceinline__ void stage_cols(T* dst, const T* base, int64_t rs, int r0, int rend,
                                            int tid) {
-  for (int idx = tid; idx < (ROWS / 2) * (D / 8); idx += kAttnThreads) {
+  for (int idx = tid; idx < (ROWS / 2) * (D / 8); idx += NT) {
     const int p = idx % (ROWS / 2), dc = idx / (ROWS / 2);
     const int r = r0 + 2 * p;
     uint4 v0 = make_uint4(0, 0, 0, 0), v1 = make_uint4(0, 0, 0, 0);

@@ -10,8 +10,9 @@
 // dQ^T += K^T dS^T with K^T staged transposed in LDS and dS^T fed from registers in the permuted
 // key order (the forward's P V trick).
 //
-// k_attn_bwd_dkdv: one block per (128 keys, kv head, part of the kv head's query heads);
-// wavefront w owns keys 32w..32w+31 and holds their K and V in registers as B operands. It
+// k_attn_bwd_dkdv: one block per (256 keys at D = 128, 128 at D = 64; kv head; part of the kv
+// head's query heads); wavefront w owns keys 32w..32w+31 and holds their K in registers as B
+// operands (V's come from the block's V rows in LDS). It
 // walks, for each of its query heads in turn and each query tile of 64 at or after its keys
 // (the next tile prefetched into registers during the current one), S = Q K^T and dP = dO V^T (Q and dO
 // staged row-major in LDS as A operands), then dV^T += dO^T P and dK^T += Q^T dS (Q^T and dO^T
@@ -131,16 +132,16 @@ __global__ __launch_bounds__(kAttnThreads, 2) void k_attn_bwd_dq(const AttnBwdAr
 // idx = tid + 256 j, rows (2p, 2p + 1) of 8-column chunk dc (p = idx % (ROWS / 2),
 // dc = idx / (ROWS / 2)); store() writes it to LDS row-major (pitch RP) and transposed (pitch
 // CP) in one go, so each global chunk is read once for both copies.
-template <typename T, int D, int ROWS>
+template <typename T, int D, int ROWS, int NT = kAttnThreads>
 struct TilePairs {
-  static constexpr int N = (ROWS / 2) * (D / 8) / kAttnThreads;
-  static_assert(N >= 1 && (ROWS / 2) * (D / 8) % kAttnThreads == 0, "tile / block mismatch");
+  static constexpr int N = (ROWS / 2) * (D / 8) / NT;
+  static_assert(N >= 1 && (ROWS / 2) * (D / 8) % NT == 0, "tile / block mismatch");
   uint4 r0[N], r1[N];
 
   __device__ __forceinline__ void load(const T* base, int64_t rs, int t0, int tend, int tid) {
 #pragma unroll
     for (int j = 0; j < N; ++j) {
-      const int idx = tid + kAttnThreads * j;
+      const int idx = tid + NT * j;
       const int p = idx % (ROWS / 2), dc = idx / (ROWS / 2);
       const int t = t0 + 2 * p;
       r0[j] = t < tend ? *reinterpret_cast<const uint4*>(base + (int64_t)t * rs + 8 * dc)
@@ -154,7 +155,7 @@ struct TilePairs {
   __device__ __forceinline__ void store(T* rows, T* cols, int tid) const {
 #pragma unroll
     for (int j = 0; j < N; ++j) {
-      const int idx = tid + kAttnThreads * j;
+      const int idx = tid + NT * j;
       const int p = idx % (ROWS / 2), dc = idx / (ROWS / 2);
       *reinterpret_cast<uint4*>(&rows[(2 * p) * RP + 8 * dc]) = r0[j];
       *reinterpret_cast<uint4*>(&rows[(2 * p + 1) * RP + 8 * dc]) = r1[j];
@@ -170,8 +171,18 @@ struct TilePairs {
   }
 };
 
+// Wavefronts per dK / dV block: 8 (256 keys) at D = 128, 4 (128 keys) at D = 64. With V's B
+// operands read from LDS the D = 128 kernel fits 2 wavefronts per SIMD (one 8-wave block per
+// CU, its LDS ~139 KiB); the staged Q / dO tiles are then shared by 8 wavefronts.
+template <int D>
+constexpr int dkdv_waves() {
+  return D == 128 ? 8 : 4;
+}
+
 template <typename T, int D>
-__global__ __launch_bounds__(kAttnThreads) void k_attn_bwd_dkdv(const AttnBwdArgs b) {
+__global__ __launch_bounds__(64 * dkdv_waves<D>(), 2) void k_attn_bwd_dkdv(const AttnBwdArgs b) {
+  constexpr int NW = dkdv_waves<D>();
+  constexpr int NT = 64 * NW, BK = 32 * NW;
   using V8 = typename Mfma<T>::v8;
   const AttnArgs& a = b.f;
   constexpr int BQ = kAttnBQ;
@@ -182,15 +193,16 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_bwd_dkdv(const AttnBwdArg
   __shared__ __align__(16) T qt_[D * CP];   // Q^T (A operand of dK^T)
   __shared__ __align__(16) T dt_[D * CP];   // dO^T (A operand of dV^T)
   __shared__ float lse_s[BQ], del_s[BQ];
+  __shared__ __align__(16) T vsm[BK * RP];  // this block's V rows (B operands of dP)
 
   const int seq = blockIdx.z;
   const int split = b.split;                 // query-head groups per kv head
   const int kh = blockIdx.y / split, part = blockIdx.y % split;
   int start, end;
   seq_bounds(a.cu, seq, a.T, &start, &end);
-  const int ntiles = (end - start + kAttnBK - 1) / kAttnBK;
+  const int ntiles = (end - start + BK - 1) / BK;
   if ((int)blockIdx.x >= ntiles) return;
-  const int k0 = start + (int)blockIdx.x * kAttnBK;  // early key tiles see the most queries
+  const int k0 = start + (int)blockIdx.x * BK;  // early key tiles see the most queries
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int lq = lane & 31, hi = lane >> 5;
   const int kw0 = k0 + 32 * w;  // this wavefront's first key
@@ -200,18 +212,17 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_bwd_dkdv(const AttnBwdArg
   const int gs = a.HQ / a.HK / split;          // query heads of this block
   const int h0 = kh * (a.HQ / a.HK) + part * gs;
 
-  // K and V of this lane's key as B operands (B[d][key] = K[key][d]).
-  V8 kb[D / 16], vb[D / 16];
+  // K of this lane's key as B operands in registers (B[d][key] = K[key][d]); the block's V rows
+  // in LDS, read as the B operands of dP (published by the first barrier of the loop).
+  V8 kb[D / 16];
   {
-    const int64_t col = (int64_t)kh * D + 8 * hi;
-    const T* krow = static_cast<const T*>(a.k) + (int64_t)kj * a.k_rs + col;
-    const T* vrow = static_cast<const T*>(a.v) + (int64_t)kj * a.v_rs + col;
+    const T* krow = static_cast<const T*>(a.k) + (int64_t)kj * a.k_rs + (int64_t)kh * D + 8 * hi;
 #pragma unroll
-    for (int c = 0; c < D / 16; ++c) {
-      kb[c] = kok ? ld16<V8>(krow + 16 * c) : V8{};
-      vb[c] = kok ? ld16<V8>(vrow + 16 * c) : V8{};
-    }
+    for (int c = 0; c < D / 16; ++c) kb[c] = kok ? ld16<V8>(krow + 16 * c) : V8{};
   }
+  stage_rows<T, D, BK, RP, NT>(vsm, static_cast<const T*>(a.v) + (int64_t)kh * D, a.v_rs, k0, end,
+                               tid);
+  const T* vlds = &vsm[(32 * w + lq) * RP + 8 * hi];
   f32x16 dka[D / 32], dva[D / 32];
 #pragma unroll
   for (int md = 0; md < D / 32; ++md) dka[md] = dva[md] = f32x16{};
@@ -220,7 +231,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_bwd_dkdv(const AttnBwdArg
   // into registers while the current one is computed.
   const int nqt = (end - k0 + BQ - 1) / BQ;
   const int items = gs * nqt;
-  TilePairs<T, D, BQ> pq, pd;
+  TilePairs<T, D, BQ, NT> pq, pd;
   float lse_n = 0.f, del_n = 0.f;
   auto prefetch = [&](int it) {
     const int h = h0 + it / nqt, qt = k0 + (it % nqt) * BQ;
@@ -258,7 +269,7 @@ __global__ __launch_bounds__(kAttnThreads) void k_attn_bwd_dkdv(const AttnBwdArg
 #pragma unroll
       for (int c = 0; c < D / 16; ++c) {
         s = Mfma<T>::run(ld16<V8>(qrow + 16 * c), kb[c], s);
-        dp = Mfma<T>::run(ld16<V8>(drow + 16 * c), vb[c], dp);
+        dp = Mfma<T>::run(ld16<V8>(drow + 16 * c), ld16<V8>(vlds + 16 * c), dp);
       }
       // s[i] is S[q][kj] for query row r = 32 qh + 8 (i / 4) + 4 hi + i % 4 of the tile
       V8 pb[2], sb_[2];
@@ -338,8 +349,9 @@ hipError_t bwd_run(const AttnBwdArgs& b, int max_seqlen, hipStream_t s) {
   hipLaunchKernelGGL((k_attn_bwd_dq<T, D>), gq, dim3(kAttnThreads), 0, s, b);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  const dim3 gk((max_seqlen + kAttnBK - 1) / kAttnBK, b.f.HK * b.split, b.f.n_seq);
-  hipLaunchKernelGGL((k_attn_bwd_dkdv<T, D>), gk, dim3(kAttnThreads), 0, s, b);
+  constexpr int NW = dkdv_waves<D>();
+  const dim3 gk((max_seqlen + 32 * NW - 1) / (32 * NW), b.f.HK * b.split, b.f.n_seq);
+  hipLaunchKernelGGL((k_attn_bwd_dkdv<T, D>), gk, dim3(64 * NW), 0, s, b);
   e = hipGetLastError();
   if (e != hipSuccess || b.split == 1) return e;
   const int64_t quads = b.f.T * b.f.HK * D / 4;

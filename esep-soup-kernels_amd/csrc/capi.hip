@@ -71,13 +71,13 @@ int64_t bwd_partials(int64_t rows, int64_t n) {
 }
 
 // Blocks per (kv head, key tile) of the attention dK / dV kernel: split the kv head's query
-// heads over more blocks (the smallest divisor of HQ / HK that gives >= 512 blocks for T tokens),
-// each writing fp32 partials, when one block per kv head would leave the GPU half empty.
+// heads over more blocks (the smallest divisor of HQ / HK that gives >= 256 blocks for T tokens,
+// one per CU), each writing fp32 partials, when one block per kv head would leave CUs idle.
 int attn_split(int64_t T, int HQ, int HK) {
   const int G = HQ / HK;
-  const int64_t blocks = ((T + esep::kAttnBK - 1) / esep::kAttnBK) * HK;
+  const int64_t blocks = ((T + 255) / 256) * HK;  // 256-key blocks (the D = 128 kernel)
   int s = 1;
-  while (blocks * s < 512 && s < G) {
+  while (blocks * s < 256 && s < G) {
     ++s;
     while (G % s) ++s;
   }
