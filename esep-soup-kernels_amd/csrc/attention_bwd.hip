@@ -30,11 +30,12 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-template <typename T, int D>
 // 2 wavefronts per SIMD without spills (unbounded, the compiler settles at 1).
-__global__ __launch_bounds__(kAttnThreads, 2) void k_attn_bwd_dq(const AttnBwdArgs b) {
+template <typename T, int D, int NW>
+__global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq(const AttnBwdArgs b) {
   using V8 = typename Mfma<T>::v8;
   const AttnArgs& a = b.f;
+  constexpr int NT = 64 * NW, BM = 32 * NW;  // queries per block
   constexpr int BN = kAttnBN;
   constexpr int KP = D + 8;
   constexpr int TP = BN + 8;
@@ -45,9 +46,9 @@ __global__ __launch_bounds__(kAttnThreads, 2) void k_attn_bwd_dq(const AttnBwdAr
   const int seq = blockIdx.z, h = blockIdx.y;
   int start, end;
   seq_bounds(a.cu, seq, a.T, &start, &end);
-  const int ntiles = (end - start + kAttnBM - 1) / kAttnBM;
+  const int ntiles = (end - start + BM - 1) / BM;
   if ((int)blockIdx.x >= ntiles) return;
-  const int q0 = start + (ntiles - 1 - (int)blockIdx.x) * kAttnBM;
+  const int q0 = start + (ntiles - 1 - (int)blockIdx.x) * BM;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int lq = lane & 31, hi = lane >> 5;
   const int kvh = h / (a.HQ / a.HK);
@@ -81,15 +82,15 @@ __global__ __launch_bounds__(kAttnThreads, 2) void k_attn_bwd_dq(const AttnBwdAr
   f32x16 dqa[D / 32];
 #pragma unroll
   for (int md = 0; md < D / 32; ++md) dqa[md] = f32x16{};
-  const int kend = end < q0 + kAttnBM ? end : q0 + kAttnBM;
+  const int kend = end < q0 + BM ? end : q0 + BM;
   const T* kbase = static_cast<const T*>(a.k) + (int64_t)kvh * D;
   const T* vbase = static_cast<const T*>(a.v) + (int64_t)kvh * D;
 
   for (int kt = start; kt < kend; kt += BN) {
     __syncthreads();
-    stage_rows<T, D, BN, KP>(ks, kbase, a.k_rs, kt, kend, tid);
-    stage_rows<T, D, BN, KP>(vs, vbase, a.v_rs, kt, kend, tid);
-    stage_cols<T, D, BN, TP>(kt_, kbase, a.k_rs, kt, kend, tid);
+    stage_rows<T, D, BN, KP, NT>(ks, kbase, a.k_rs, kt, kend, tid);
+    stage_rows<T, D, BN, KP, NT>(vs, vbase, a.v_rs, kt, kend, tid);
+    stage_cols<T, D, BN, TP, NT>(kt_, kbase, a.k_rs, kt, kend, tid);
     __syncthreads();
     if (!wave_live || kt > wq_last) continue;
 
@@ -345,8 +346,11 @@ __global__ __launch_bounds__(256) void k_attn_dkdv_reduce(const AttnBwdArgs b, i
 
 template <typename T, int D>
 hipError_t bwd_run(const AttnBwdArgs& b, int max_seqlen, hipStream_t s) {
-  const dim3 gq((max_seqlen + kAttnBM - 1) / kAttnBM, b.f.HQ, b.f.n_seq);
-  hipLaunchKernelGGL((k_attn_bwd_dq<T, D>), gq, dim3(kAttnThreads), 0, s, b);
+  // 4 wavefronts (128 queries) per dQ block: 8 measured slower (with 256 causal queries per
+  // block the early wavefronts idle through the later key tiles).
+  constexpr int QW = 4;
+  const dim3 gq((max_seqlen + 32 * QW - 1) / (32 * QW), b.f.HQ, b.f.n_seq);
+  hipLaunchKernelGGL((k_attn_bwd_dq<T, D, QW>), gq, dim3(64 * QW), 0, s, b);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   constexpr int NW = dkdv_waves<D>();

@@ -117,3 +117,52 @@ def test_partition_depends_on_shape_only(rows, n):
     p = _hip.rmsnorm_partials(rows, n)
     assert 1 <= p <= 256 and p == _hip.rmsnorm_partials(rows, n)
     assert _hip.rmsnorm_partials(0, n) == 0
+
+
+def test_attention_validation():
+    """esep_attn_fwd / esep_attn_bwd reject bad arguments before launching anything."""
+    lib = _hip.lib()
+
+    def fwd(**kw):
+        a = dict(q=16, q_rs=256, k=16, k_rs=256, v=16, v_rs=256, o=16, o_rs=256, lse=None, dt=2,
+                 T=4, HQ=2, HK=2, D=128, cu=16, n_seq=1, max_seqlen=4, scale=0.1, stream=None)
+        a.update(kw)
+        return lib.esep_attn_fwd(*a.values())
+
+    assert fwd(dt=0) == -1 and b"dtype" in lib.esep_last_error()  # fp32 not taken
+    assert fwd(D=96) == -2
+    assert fwd(HQ=3, HK=2) == -2  # query heads must be a multiple of kv heads
+    assert fwd(q_rs=128) == -2  # token stride below HQ * D
+    assert fwd(q=None) == -1
+    assert fwd(cu=None) == -1
+    assert fwd(q=8) == -3 and b"alignment" in lib.esep_last_error()
+    assert fwd(q_rs=260) == -3
+    assert fwd(scale=0.0) == -1
+    assert fwd(T=0) == 0 and fwd(n_seq=0) == 0  # nothing to do, nothing launched
+
+    def bwd(**kw):
+        a = dict(q=16, q_rs=256, k=16, k_rs=256, v=16, v_rs=256, o=16, o_rs=256, do=16,
+                 do_rs=256, lse=16, ws=16, dq=16, dq_rs=256, dk=16, dk_rs=256, dv=16, dv_rs=256,
+                 dt=1, T=4, HQ=2, HK=2, D=128, cu=16, n_seq=1, max_seqlen=4, scale=0.1,
+                 stream=None)
+        a.update(kw)
+        return lib.esep_attn_bwd(*a.values())
+
+    assert bwd(dt=4) == -1
+    assert bwd(lse=None) == -1 and bwd(ws=None) == -1
+    assert bwd(dk=None) == -1
+    assert bwd(ws=8) == -3
+    assert bwd(dv_rs=100) == -2
+    assert bwd(T=0) == 0
+
+
+def test_attention_workspace_size():
+    """Per-query delta (rounded up to 4 floats) plus the dK/dV partials when the query heads of a
+    kv head are split over blocks: a pure function of the shape."""
+    ws = _hip.attn_bwd_workspace
+    assert ws(0, 12, 2, 128) == 0 and ws(8, 3, 2, 128) == 0
+    # 1 sequence of 65536 tokens, 28/4 heads: 256-key blocks already fill the GPU, no split
+    assert ws(65536, 28, 4, 128) == 28 * 65536
+    # 8192 tokens, 12/2 heads: 32 x 2 blocks, split over all 6 query heads of a kv head
+    assert ws(8192, 12, 2, 128) == 12 * 8192 + 2 * 6 * 8192 * 2 * 128
+    assert ws(3, 1, 1, 64) == 4  # delta rounded up to a multiple of 4 floats
