@@ -8,6 +8,7 @@
 #include "esep_body.h"
 #include "rmsnorm.hpp"
 #include "rope.hpp"
+#include "swiglu.hpp"
 
 namespace {
 
@@ -480,6 +481,40 @@ int esep_attn_bwd(const void* q, int64_t q_rs, const void* k, int64_t k_rs, cons
   const hipError_t e = esep::launch_attn_bwd(b, dt, D, max_seqlen, static_cast<hipStream_t>(stream), &sup);
   if (!sup) return fail(ESEP_EINVAL, "attn_bwd: unsupported dtype / D");
   return e == hipSuccess ? 0 : hip_fail(e, "attn_bwd launch");
+}
+
+int esep_swiglu_fwd(const void* gate, const void* up, void* out, int64_t n, int dt,
+                    void* stream) {
+  g_err[0] = 0;
+  if (!float_dt(dt)) return fail(ESEP_EINVAL, "swiglu_fwd: bad dtype code %d", dt);
+  if (n < 0) return fail(ESEP_ESHAPE, "swiglu_fwd: n=%lld < 0", (long long)n);
+  if (n == 0) return 0;
+  if (gate == nullptr || up == nullptr || out == nullptr)
+    return fail(ESEP_EINVAL, "swiglu_fwd: gate, up and out are required");
+  if (!aligned16(gate) || !aligned16(up) || !aligned16(out))
+    return fail(ESEP_EALIGN, "swiglu_fwd: tensors need 16-byte alignment");
+  bool sup = false;
+  const hipError_t e = esep::launch_swiglu_fwd(gate, up, out, n, dt, static_cast<hipStream_t>(stream), &sup);
+  if (!sup) return fail(ESEP_EINVAL, "swiglu_fwd: unsupported dtype");
+  return e == hipSuccess ? 0 : hip_fail(e, "swiglu_fwd launch");
+}
+
+int esep_swiglu_bwd(const void* dout, const void* gate, const void* up, void* dgate, void* dup,
+                    int64_t n, int dt, void* stream) {
+  g_err[0] = 0;
+  if (!float_dt(dt)) return fail(ESEP_EINVAL, "swiglu_bwd: bad dtype code %d", dt);
+  if (n < 0) return fail(ESEP_ESHAPE, "swiglu_bwd: n=%lld < 0", (long long)n);
+  if (n == 0) return 0;
+  if (dout == nullptr || gate == nullptr || up == nullptr || dgate == nullptr || dup == nullptr)
+    return fail(ESEP_EINVAL, "swiglu_bwd: dout, gate, up, dgate and dup are required");
+  if (!aligned16(dout) || !aligned16(gate) || !aligned16(up) || !aligned16(dgate) || !aligned16(dup))
+    return fail(ESEP_EALIGN, "swiglu_bwd: tensors need 16-byte alignment");
+  if (dgate == dup) return fail(ESEP_EINVAL, "swiglu_bwd: dgate and dup must not alias");
+  bool sup = false;
+  const hipError_t e = esep::launch_swiglu_bwd(dout, gate, up, dgate, dup, n, dt,
+                                               static_cast<hipStream_t>(stream), &sup);
+  if (!sup) return fail(ESEP_EINVAL, "swiglu_bwd: unsupported dtype");
+  return e == hipSuccess ? 0 : hip_fail(e, "swiglu_bwd launch");
 }
 
 }  // extern "C"

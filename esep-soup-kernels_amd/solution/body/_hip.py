@@ -45,6 +45,8 @@ SIGNATURES = {
     "esep_attn_fwd": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i32, _i64, _i32,
                              _i32, _i32, _vp, _i32, _i32, _f32, _vp]),
     "esep_attn_bwd_workspace": (_i64, [_i64, _i32, _i32, _i32]),
+    "esep_swiglu_fwd": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp]),
+    "esep_swiglu_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _vp]),
     "esep_attn_bwd": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp,
                              _vp, _i64, _vp, _i64, _vp, _i64, _i32, _i64, _i32, _i32, _i32, _vp,
                              _i32, _i32, _f32, _vp]),
@@ -351,4 +353,40 @@ def attn_bwd(q, k, v, o, dout, lse, dq, dk, dv, cu_seqlens, max_seqlen, scale, w
         dtype_code(q.dtype), T, HQ, HK, D, _p(cu_seqlens), cu_seqlens.numel() - 1,
         int(max_seqlen), float(scale), _stream(dev))
     _check(rc, "esep_attn_bwd")
+    _record(name)
+
+
+def _flat(t, name):
+    if not t.is_contiguous():
+        raise EsepError(f"{name} must be contiguous")
+    return t
+
+
+def swiglu_fwd(gate, up, out, name="_swiglu_fwd"):
+    """out = silu(gate) * up (esep_swiglu_fwd); contiguous tensors of one dtype and size; out
+    may be gate itself."""
+    dev = _dev(gate, up, out)
+    if gate.numel() != up.numel() or gate.numel() != out.numel():
+        raise EsepError("gate, up and out must have the same number of elements")
+    if up.dtype != gate.dtype or out.dtype != gate.dtype:
+        raise EsepError("gate, up and out must share one dtype")
+    rc = lib().esep_swiglu_fwd(_p(_flat(gate, "gate")), _p(_flat(up, "up")), _p(_flat(out, "out")),
+                               gate.numel(), dtype_code(gate.dtype), _stream(dev))
+    _check(rc, "esep_swiglu_fwd")
+    _record(name)
+
+
+def swiglu_bwd(dout, gate, up, dgate, dup, name="_swiglu_bwd"):
+    """(dgate, dup) of out = silu(gate) * up (esep_swiglu_bwd); dgate may be gate and dup may
+    be up."""
+    dev = _dev(dout, gate, up, dgate, dup)
+    n = gate.numel()
+    if any(t.numel() != n for t in (dout, up, dgate, dup)):
+        raise EsepError("dout, gate, up, dgate and dup must have the same number of elements")
+    if any(t.dtype != gate.dtype for t in (dout, up, dgate, dup)):
+        raise EsepError("dout, gate, up, dgate and dup must share one dtype")
+    rc = lib().esep_swiglu_bwd(_p(_flat(dout, "dout")), _p(_flat(gate, "gate")), _p(_flat(up, "up")),
+                               _p(_flat(dgate, "dgate")), _p(_flat(dup, "dup")), n,
+                               dtype_code(gate.dtype), _stream(dev))
+    _check(rc, "esep_swiglu_bwd")
     _record(name)

@@ -20,9 +20,13 @@ kernel takes, as the reference's do):
   _attention  attention.varlen_attention: causal attention over all rows in one launch per
               direction (fp16 / bf16, head_dim 64 or 128, no dropout); else the reference's
               per-row SDPA loop.
-The rest of the layer (q/k/v/o projections, MLP) calls the model's own modules: the
-reference's NF4 / LoRA / recompute-MLP routes (packed.py:184-352, :440-693) are other
-workstreams and are not part of this build; their flags exist for API compatibility.
+  _mlp        frozen projections: _RecomputeMLP (saves no [T, intermediate] tensor, recomputes
+              the gate / up projections and, when the norm did not save its output, the norm
+              itself in backward); otherwise the model's projections with silu(g) * u on the
+              HIP SwiGLU kernel (solution/swiglu.py).
+The q/k/v/o projections call the model's own modules: the reference's NF4 / LoRA routes
+(packed.py:184-352, :440-524) are other workstreams and are not part of this build; their flags
+exist for API compatibility.
 """
 
 import contextlib
@@ -41,8 +45,9 @@ _IGNORED_KWARGS = {"num_items_in_batch", "return_dict", "output_attentions",
 # In-process switches (never read from the environment), as in the reference: USE_KERNELS
 # (packed.py:106) turns the HIP norm / RoPE off (packed layout on torch ops);
 # NORM_SAVE_OUTPUT (:149) makes the decoder-layer norms save their 16-bit output instead of the
-# fp32 residual; USE_LORA_KERNELS (:186) and RECOMPUTE_MLP (:448) select routes that this build
-# does not have (kept so code that sets them keeps working).
+# fp32 residual; RECOMPUTE_MLP (:448) sends an MLP with frozen projections through
+# _RecomputeMLP; USE_LORA_KERNELS (:186) selects a route this build does not have (kept so code
+# that sets it keeps working).
 USE_KERNELS = True
 NORM_SAVE_OUTPUT = True
 USE_LORA_KERNELS = True
@@ -238,10 +243,117 @@ def _attention(attn, q, k, v, lens):
     return out.reshape(1, out.shape[0], hq * d)
 
 
-def _mlp(mlp, xs):
+def _plain_silu_mlp(mlp, x):
+    """An unmodified Qwen2MLP with silu and no hooks, on a CUDA input."""
+    from transformers.models.qwen2.modeling_qwen2 import Qwen2MLP
+
+    return (type(mlp) is Qwen2MLP and not _has_hooks(mlp) and x.is_cuda
+            and getattr(getattr(mlp, "config", None), "hidden_act", None) == "silu")
+
+
+def _mlp_layers(mlp, x):
+    """(gate, up, down) when the recompute MLP applies to mlp(x), else None (reference
+    packed.py:493-524, there for frozen NF4 projections): kernels and RECOMPUTE_MLP on, grad
+    mode on, an unmodified silu Qwen2MLP whose projections are exactly nn.Linear without bias
+    or hooks, no trainable parameter in the block, and an fp16 / bf16 CUDA x that the
+    projections compute in (autocast to x's dtype, or weights of x's dtype)."""
+    if not (USE_KERNELS and RECOMPUTE_MLP) or not torch.is_grad_enabled():
+        return None
+    why = "recompute MLP"
+    if x.dtype not in (torch.float16, torch.bfloat16) or not _plain_silu_mlp(mlp, x):
+        return _fallback(why, f"x {x.dtype}, {type(mlp).__name__}, hooks or activation")
+    layers = (getattr(mlp, "gate_proj", None), getattr(mlp, "up_proj", None),
+              getattr(mlp, "down_proj", None))
+    autocast = torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == x.dtype
+    for lin in layers:
+        if type(lin) is not torch.nn.Linear or _has_hooks(lin) or lin.bias is not None:
+            return _fallback(why, "projection not a plain bias-free nn.Linear")
+        if not autocast and lin.weight.dtype != x.dtype:
+            return _fallback(why, f"weights {lin.weight.dtype} without autocast to {x.dtype}")
+    if any(q.requires_grad for q in mlp.parameters()):
+        return _fallback(why, "trainable parameter in the MLP")
+    return layers
+
+
+class _RecomputeMLP(torch.autograd.Function):
+    """down(silu(gate(x)) * up(x)) for frozen projections, saving nothing of size
+    [T, intermediate] (reference packed.py:562-643; there the projections are frozen NF4, here
+    frozen fp16 / bf16 nn.Linear, as in a LoRA run on an unquantized base).
+
+    forward: g = x Wg^T, u = x Wu^T, h = silu(g) * u (HIP kernel, in place into g), out = h Wd^T.
+    Saved: x itself (when the norm saves its output, the same tensor: no extra memory), or the
+    norm's fp32 input r and weight, x then recomputed in backward by the same norm kernel
+    (bit-exact, norm_rope.rmsnorm_recompute).
+    backward: dh = dout Wd; g, u recomputed; (dg, du) = swiglu backward (HIP kernel, in place
+    into g, u); dx_gate = dg Wg, dx_up = du Wu, returned as the grads of the two fan-out copies
+    x_gate, x_up (the norm backward sums them; one tensor for both: autograd sums them).
+    """
+
+    @staticmethod
+    @torch.amp.custom_fwd(device_type="cuda")
+    def forward(ctx, x, x_up, r, w_norm, eps, gate, up, down):
+        from . import _hip
+
+        shape = x.shape
+        x2 = x.reshape(-1, shape[-1])
+        g = F.linear(x2, gate.weight).contiguous()
+        u = F.linear(x2, up.weight).contiguous()
+        _hip.swiglu_fwd(g, u, g)
+        del u
+        out = F.linear(g, down.weight)
+        del g
+        if r is not None:
+            ctx.save_for_backward(r, w_norm)
+        else:
+            ctx.save_for_backward(x2)
+        ctx.recompute_x = r is not None
+        ctx.eps, ctx.shape, ctx.dtype, ctx.layers = eps, shape, x.dtype, (gate, up, down)
+        return out.view(*shape[:-1], out.shape[-1])
+
+    @staticmethod
+    @torch.amp.custom_bwd(device_type="cuda")
+    def backward(ctx, dout):
+        from . import _hip
+
+        gate, up, down = ctx.layers
+        if ctx.recompute_x:
+            from .norm_rope import rmsnorm_recompute
+
+            r, w_norm = ctx.saved_tensors
+            x2 = rmsnorm_recompute(r.reshape(-1, r.shape[-1]), w_norm, ctx.eps, ctx.dtype)
+        else:
+            (x2,) = ctx.saved_tensors
+        dh = torch.matmul(dout.reshape(-1, dout.shape[-1]), down.weight)
+        g = F.linear(x2, gate.weight).contiguous()
+        u = F.linear(x2, up.weight).contiguous()
+        del x2
+        dh = dh.to(g.dtype).contiguous()
+        _hip.swiglu_bwd(dh, g, u, g, u)  # dg into g, du into u
+        del dh
+        dx_gate = torch.matmul(g, gate.weight).to(ctx.dtype)
+        del g
+        dx_up = torch.matmul(u, up.weight).to(ctx.dtype)
+        return dx_gate.view(ctx.shape), dx_up.view(ctx.shape), None, None, None, None, None, None
+
+
+def _mlp(mlp, xs, norm=None, residual=None, eps=None, norm_saves_y=False):
     """Qwen2MLP on the post-attention norm's two outputs (gate, up): each projection takes its
-    own copy, so the norm backward sums their input gradients."""
+    own copy, so the norm backward sums their input gradients (reference packed.py:676-693).
+    Frozen projections: _RecomputeMLP (x recomputed from the norm's residual when the norm did
+    not save its output). Otherwise, with the kernels on, the projections as the model's modules
+    and silu(g) * u on the HIP kernel; else HF's ops."""
     x_gate, x_up = xs if isinstance(xs, tuple) else (xs, xs)
+    layers = _mlp_layers(mlp, x_gate)
+    if layers is not None:
+        r = w_norm = None
+        if (eps is not None and not norm_saves_y and residual is not None
+                and residual.dtype == torch.float32 and residual.is_contiguous()):
+            r, w_norm = residual, norm.weight.detach().to(torch.float32)
+        return _RecomputeMLP.apply(x_gate, x_up, r, w_norm, eps, *layers)
+    if USE_KERNELS and _plain_silu_mlp(mlp, x_gate):
+        from ..swiglu import swiglu
+
+        return mlp.down_proj(swiglu(mlp.gate_proj(x_gate), mlp.up_proj(x_up)))
     return mlp.down_proj(mlp.act_fn(mlp.gate_proj(x_gate)) * mlp.up_proj(x_up))
 
 
@@ -259,9 +371,10 @@ def _layer(layer, residual, delta, rope_in, lens):
     v = attn.v_proj(x_v).view(1, n, -1, hd)
     q, k = _rope(q, k, rope_in)
     o = attn.o_proj(_attention(attn, q, k, v, lens))
-    residual, xs = _add_norm(layer.post_attention_layernorm, residual, o, n_out=2,
-                             save_output=NORM_SAVE_OUTPUT)
-    return residual, _mlp(layer.mlp, xs)
+    norm = layer.post_attention_layernorm
+    residual, xs, eps = _add_norm(norm, residual, o, with_eps=True, n_out=2,
+                                  save_output=NORM_SAVE_OUTPUT)
+    return residual, _mlp(layer.mlp, xs, norm, residual, eps, norm_saves_y=NORM_SAVE_OUTPUT)
 
 
 def _unsupported(model, input_ids, attention_mask, past_key_values, inputs_embeds, use_cache,

@@ -216,6 +216,21 @@ int esep_attn_bwd(const void* q, int64_t q_rs, const void* k, int64_t k_rs, cons
                   int D, const int32_t* cu_seqlens, int n_seq, int max_seqlen, float scale,
                   void* stream);
 
+/*
+ * SwiGLU of the Qwen2 MLP, element-wise over n elements of one dtype (fp32 / fp16 / bf16),
+ * contiguous, 16-byte aligned. Replaces the example kernels the reference decoder calls,
+ * solution/swiglu.py:15-37 (example_swiglu_fwd_kernel / example_swiglu_bwd_kernel, launched at
+ * swiglu.py:49-50, :59-60 and solution/body/packed.py:538, :558):
+ *   s = sigmoid(gate) in fp32;  out = gate * s * up
+ *   dup = dout * gate * s;  dgate = dout * up * s * (1 + gate * (1 - s))
+ * out may alias gate; dgate may alias gate and dup may alias up (each element is read before it
+ * is written), as the recompute MLP uses them.
+ */
+int esep_swiglu_fwd(const void* gate, const void* up, void* out, int64_t n, int dt,
+                    void* stream);
+int esep_swiglu_bwd(const void* dout, const void* gate, const void* up, void* dgate, void* dup,
+                    int64_t n, int dt, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

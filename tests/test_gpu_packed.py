@@ -108,7 +108,7 @@ def _compare(ref, new, mask, tol_h=5e-3, tol_loss=1e-3, tol_g=2e-2):
 
 def _counts(names):
     return {k: names.count(k) for k in ("_add_rmsnorm_fwd", "_add_rmsnorm_bwd", "_rope_kernel",
-                                        "_attn_fwd", "_attn_bwd")}
+                                        "_attn_fwd", "_attn_bwd", "_swiglu_fwd", "_swiglu_bwd")}
 
 
 @pytest.mark.parametrize("kernels", [True, False], ids=["kernels", "torch"])
@@ -139,6 +139,8 @@ def test_packed_matches_original(variant, left, kernels, dtype):
         assert c["_rope_kernel"] == 3 * n_layers, c
         # one varlen attention launch per layer and direction (loss forward + hidden forward)
         assert c["_attn_fwd"] == 2 * n_layers and c["_attn_bwd"] == n_layers, c
+        # SwiGLU on the HIP kernel: through the recompute MLP when the MLP is frozen
+        assert c["_swiglu_fwd"] == 2 * n_layers and c["_swiglu_bwd"] == n_layers, c
     else:
         assert not any(c.values()), c
 
@@ -212,3 +214,31 @@ def test_patch_is_idempotent():
     fwd = modeling_qwen2.Qwen2Model.forward
     patch()
     assert modeling_qwen2.Qwen2Model.forward is fwd and hasattr(fwd, "__wrapped__")
+
+
+@pytest.mark.parametrize("save_output", [True, False], ids=["norm_saves_y", "recompute_norm"])
+def test_packed_recompute_mlp(save_output, monkeypatch):
+    """Frozen MLP through the recompute MLP, with the post-attention norm saving its output (x
+    saved as is) or not (x recomputed from the fp32 residual by the norm kernel in backward,
+    reference test_body_recompute.py:192-219); against HF's original forward and with the
+    recompute MLP switched off."""
+    from solution.body import _hip, packed, patch
+
+    patch()
+    model = _build("frozen")
+    ids, mask, labels = _batch()
+    with _original_forward():
+        ref = _run(model, ids, mask, labels)
+    monkeypatch.setattr(packed, "NORM_SAVE_OUTPUT", save_output)
+    with _hip.count_launches() as names:
+        new = _run(model, ids, mask, labels)
+    _compare(ref, new, mask)
+    n_layers = model.config.num_hidden_layers
+    c = _counts(names)
+    assert c["_swiglu_fwd"] == 2 * n_layers and c["_swiglu_bwd"] == n_layers, c
+    # recompute from the residual: one more norm forward per layer in the backward
+    extra = 0 if save_output else n_layers
+    assert c["_add_rmsnorm_fwd"] == 2 * (2 * n_layers + 1) + extra, c
+    monkeypatch.setattr(packed, "RECOMPUTE_MLP", False)
+    off = _run(model, ids, mask, labels)
+    _compare(ref, off, mask)
