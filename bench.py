@@ -417,6 +417,40 @@ def run_attention(dev, reps):
             "peak_TFLOP/s": PEAK_BF16_TFLOPS, **out}
 
 
+def run_swiglu(dev, reps, n_sets=4):
+    """The SwiGLU kernels at the Qwen2.5-1.5B MLP shape (T = 8192 tokens, intermediate 8960,
+    bf16): forward reads gate and up and writes h (3 x 2 bytes per element), backward reads
+    dh, gate, up and writes dgate, dup (5 x 2 bytes). Graphs over n_sets distinct buffers."""
+    import torch
+
+    from solution.body import _hip
+
+    T, I = CFG4["B"] * CFG4["S"], 8960
+    g = torch.Generator(device=dev).manual_seed(13)
+    rn = lambda: torch.randn(T, I, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    sets = [dict(g=rn(), u=rn(), d=rn()) for _ in range(n_sets)]
+    for s_ in sets:
+        s_["h"], s_["dg"], s_["du"] = (torch.empty(T, I, device=dev, dtype=torch.bfloat16) for _ in range(3))
+    out = {}
+    for kind, fn, nbytes in (
+            ("fwd", lambda: [_hip.swiglu_fwd(s_["g"], s_["u"], s_["h"]) for s_ in sets], 3 * 2 * T * I),
+            ("bwd", lambda: [_hip.swiglu_bwd(s_["d"], s_["g"], s_["u"], s_["dg"], s_["du"]) for s_ in sets],
+             5 * 2 * T * I)):
+        gr = capture(fn)
+        time_graph(gr, 2)
+        ms, _ = time_graph(gr, reps)
+        us = ms * 1e3 / n_sets
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[kind] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4),
+                     "bytes": nbytes}
+        log(f"swiglu {kind}: {us:.1f} us, {gbs:.0f} GB/s = {gbs / PEAK_GBS:.1%} of peak")
+        del gr
+    del sets
+    torch.cuda.empty_cache()
+    return {"workload": "SwiGLU silu(gate) * up of the Qwen2.5-1.5B MLP, T=8192, intermediate 8960, "
+                        "bf16, forward and backward", **out}
+
+
 def kernel_rooflines(body, reps):
     """Per-launch time of each entry point: a graph of one launch per layer of that kernel
     alone (distinct tensors, as in the sweep), replayed `reps` times, timed with HIP events
@@ -570,6 +604,7 @@ def main():
     c5 = None if args.no_config5 else run_config5(dev, max(args.steps // 3, 5))
     api = run_api_variant(dev, max(args.steps // 3, 5))
     attn = None if args.no_attention else run_attention(dev, max(args.steps // 3, 5))
+    swi = run_swiglu(dev, max(args.steps // 3, 5))
 
     cpu = None
     if not args.no_cpu:
@@ -598,6 +633,7 @@ def main():
         "config5": c5,
         "api_variant": api,
         "attention": attn,
+        "swiglu": swi,
     }
     print(json.dumps(out), flush=True)
     return 0
