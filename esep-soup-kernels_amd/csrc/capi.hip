@@ -5,6 +5,7 @@
 #include <stdio.h>
 
 #include "attention.hpp"
+#include "dropout.hpp"
 #include "esep_body.h"
 #include "rmsnorm.hpp"
 #include "rope.hpp"
@@ -515,6 +516,43 @@ int esep_swiglu_bwd(const void* dout, const void* gate, const void* up, void* dg
                                                static_cast<hipStream_t>(stream), &sup);
   if (!sup) return fail(ESEP_EINVAL, "swiglu_bwd: unsupported dtype");
   return e == hipSuccess ? 0 : hip_fail(e, "swiglu_bwd launch");
+}
+
+int esep_lora_dropout_fwd(const void* x, const int64_t* key, void* xd, int64_t n, float p, int dt,
+                          void* stream) {
+  g_err[0] = 0;
+  if (!float_dt(dt)) return fail(ESEP_EINVAL, "lora_dropout_fwd: bad dtype code %d", dt);
+  if (n < 0) return fail(ESEP_ESHAPE, "lora_dropout_fwd: n=%lld < 0", (long long)n);
+  if (!(p > 0.f && p < 1.f)) return fail(ESEP_EINVAL, "lora_dropout_fwd: p must be in (0, 1)");
+  if (n == 0) return 0;
+  if (x == nullptr || key == nullptr || xd == nullptr)
+    return fail(ESEP_EINVAL, "lora_dropout_fwd: x, key and xd are required");
+  if (!aligned16(x) || !aligned16(xd) || (reinterpret_cast<uintptr_t>(key) & 7))
+    return fail(ESEP_EALIGN, "lora_dropout_fwd: x, xd need 16-byte and key 8-byte alignment");
+  bool sup = false;
+  const hipError_t e = esep::launch_dropout_fwd(x, key, xd, n, p, dt, static_cast<hipStream_t>(stream), &sup);
+  if (!sup) return fail(ESEP_EINVAL, "lora_dropout_fwd: unsupported dtype");
+  return e == hipSuccess ? 0 : hip_fail(e, "lora_dropout_fwd launch");
+}
+
+int esep_lora_dropout_bwd(const void* x, const void* g, const int64_t* key, void* xd, void* dx,
+                          int64_t n, float p, int accumulate, int dt, void* stream) {
+  g_err[0] = 0;
+  if (!float_dt(dt)) return fail(ESEP_EINVAL, "lora_dropout_bwd: bad dtype code %d", dt);
+  if (n < 0) return fail(ESEP_ESHAPE, "lora_dropout_bwd: n=%lld < 0", (long long)n);
+  if (!(p > 0.f && p < 1.f)) return fail(ESEP_EINVAL, "lora_dropout_bwd: p must be in (0, 1)");
+  if (n == 0) return 0;
+  if (x == nullptr || g == nullptr || key == nullptr || xd == nullptr || dx == nullptr)
+    return fail(ESEP_EINVAL, "lora_dropout_bwd: x, g, key, xd and dx are required");
+  if (!aligned16(x) || !aligned16(g) || !aligned16(xd) || !aligned16(dx) ||
+      (reinterpret_cast<uintptr_t>(key) & 7))
+    return fail(ESEP_EALIGN, "lora_dropout_bwd: tensors need 16-byte and key 8-byte alignment");
+  if (xd == dx || xd == g) return fail(ESEP_EINVAL, "lora_dropout_bwd: xd must not alias g or dx");
+  bool sup = false;
+  const hipError_t e = esep::launch_dropout_bwd(x, g, key, xd, dx, n, p, accumulate ? 1 : 0, dt,
+                                                static_cast<hipStream_t>(stream), &sup);
+  if (!sup) return fail(ESEP_EINVAL, "lora_dropout_bwd: unsupported dtype");
+  return e == hipSuccess ? 0 : hip_fail(e, "lora_dropout_bwd launch");
 }
 
 }  // extern "C"

@@ -46,6 +46,8 @@ SIGNATURES = {
                              _i32, _i32, _vp, _i32, _i32, _f32, _vp]),
     "esep_attn_bwd_workspace": (_i64, [_i64, _i32, _i32, _i32]),
     "esep_swiglu_fwd": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp]),
+    "esep_lora_dropout_fwd": (_i32, [_vp, _vp, _vp, _i64, _f32, _i32, _vp]),
+    "esep_lora_dropout_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _f32, _i32, _i32, _vp]),
     "esep_swiglu_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _vp]),
     "esep_attn_bwd": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp,
                              _vp, _i64, _vp, _i64, _vp, _i64, _i32, _i64, _i32, _i32, _i32, _vp,
@@ -389,4 +391,36 @@ def swiglu_bwd(dout, gate, up, dgate, dup, name="_swiglu_bwd"):
                                _p(_flat(dgate, "dgate")), _p(_flat(dup, "dup")), n,
                                dtype_code(gate.dtype), _stream(dev))
     _check(rc, "esep_swiglu_bwd")
+    _record(name)
+
+
+def _key(key, dev):
+    if key.dtype != torch.int64 or key.numel() < 1 or key.device != dev:
+        raise EsepError("key must be an int64 tensor on the same device")
+    return key
+
+
+def lora_dropout_fwd(x, key, xd, p, name="_lora_dropout_fwd"):
+    """xd = x * keep / (1 - p) with keep regenerated from the int64 device key
+    (esep_lora_dropout_fwd)."""
+    dev = _dev(x, key, xd)
+    if x.dtype != xd.dtype or x.numel() != xd.numel():
+        raise EsepError("x and xd must share dtype and size")
+    rc = lib().esep_lora_dropout_fwd(_p(_flat(x, "x")), _p(_key(key, dev)), _p(_flat(xd, "xd")),
+                                     x.numel(), float(p), dtype_code(x.dtype), _stream(dev))
+    _check(rc, "esep_lora_dropout_fwd")
+    _record(name)
+
+
+def lora_dropout_bwd(x, g, key, xd, dx, p, accumulate=False, name="_lora_dropout_bwd"):
+    """xd = x * keep / (1 - p) (regenerated) and dx = [dx +] g * keep / (1 - p)
+    (esep_lora_dropout_bwd); dx may be g itself."""
+    dev = _dev(x, g, key, xd, dx)
+    n = x.numel()
+    if any(t.numel() != n or t.dtype != x.dtype for t in (g, xd, dx)):
+        raise EsepError("x, g, xd and dx must share dtype and size")
+    rc = lib().esep_lora_dropout_bwd(_p(_flat(x, "x")), _p(_flat(g, "g")), _p(_key(key, dev)),
+                                     _p(_flat(xd, "xd")), _p(_flat(dx, "dx")), n, float(p),
+                                     int(bool(accumulate)), dtype_code(x.dtype), _stream(dev))
+    _check(rc, "esep_lora_dropout_bwd")
     _record(name)

@@ -231,6 +231,23 @@ int esep_swiglu_fwd(const void* gate, const void* up, void* out, int64_t n, int 
 int esep_swiglu_bwd(const void* dout, const void* gate, const void* up, void* dgate, void* dup,
                     int64_t n, int dt, void* stream);
 
+/*
+ * Dropout on the LoRA input with the mask regenerated from a key (LoRA path of q_proj / v_proj).
+ * Replaces the reference's Triton launches at solution/body/lora.py:160-161
+ * (lora_dropout_fwd_kernel in lora_dropout) and :180-182 (lora_dropout_bwd_kernel in
+ * lora_down_bwd); kernel math follows lora.py:67-137.
+ *   keep(e) = uniform(key, e) >= p     uniform: Philox4x32-10 (Salmon et al., SC 2011) at counter
+ *                                      e / 4, word e % 4, (word >> 8) * 2^-24; key = *key (int64
+ *                                      in device memory, e.g. drawn by torch's CUDA generator)
+ *   fwd:  xd = x * keep / (1 - p)
+ *   bwd:  xd = x * keep / (1 - p) (regenerated);  dx = [dx +] g * keep / (1 - p)  (accumulate)
+ * x, xd, g, dx: n contiguous elements of dtype dt, 16-byte aligned; 0 < p < 1. dx may alias g.
+ */
+int esep_lora_dropout_fwd(const void* x, const int64_t* key, void* xd, int64_t n, float p, int dt,
+                          void* stream);
+int esep_lora_dropout_bwd(const void* x, const void* g, const int64_t* key, void* xd, void* dx,
+                          int64_t n, float p, int accumulate, int dt, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
