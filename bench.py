@@ -451,6 +451,40 @@ def run_swiglu(dev, reps, n_sets=4):
                         "bf16, forward and backward", **out}
 
 
+def run_lora_dropout(dev, reps, n_sets=4):
+    """The LoRA-dropout kernels at the q_proj LoRA input of config 4 (T = 8192 tokens x 1536,
+    bf16, p = 0.05): forward reads x and writes x_d (2 x 2 bytes per element); backward reads x
+    and g and writes x_d and dx (4 x 2 bytes)."""
+    import torch
+
+    from solution.body import _hip
+
+    T, H, p = CFG4["B"] * CFG4["S"], CFG4["H"], 0.05
+    g = torch.Generator(device=dev).manual_seed(17)
+    rn = lambda: torch.randn(T, H, generator=g, device=dev, dtype=torch.float32).to(torch.bfloat16)
+    key = torch.randint(0, 2 ** 63 - 1, (1,), device=dev, dtype=torch.int64)
+    sets = [dict(x=rn(), g=rn(), xd=torch.empty(T, H, device=dev, dtype=torch.bfloat16),
+                 dx=torch.empty(T, H, device=dev, dtype=torch.bfloat16)) for _ in range(n_sets)]
+    out = {}
+    for kind, fn, nbytes in (
+            ("fwd", lambda: [_hip.lora_dropout_fwd(s_["x"], key, s_["xd"], p) for s_ in sets], 2 * 2 * T * H),
+            ("bwd", lambda: [_hip.lora_dropout_bwd(s_["x"], s_["g"], key, s_["xd"], s_["dx"], p)
+                             for s_ in sets], 4 * 2 * T * H)):
+        gr = capture(fn)
+        time_graph(gr, 2)
+        ms, _ = time_graph(gr, reps)
+        us = ms * 1e3 / n_sets
+        gbs = nbytes / (us * 1e-6) / 1e9
+        out[kind] = {"us": round(us, 2), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4),
+                     "bytes": nbytes}
+        log(f"lora dropout {kind}: {us:.2f} us, {gbs:.0f} GB/s = {gbs / PEAK_GBS:.1%} of peak")
+        del gr
+    del sets
+    torch.cuda.empty_cache()
+    return {"workload": "LoRA dropout (Philox mask regenerated from a device key) on the q_proj LoRA "
+                        "input of config 4: T=8192 x 1536, bf16, p=0.05", **out}
+
+
 def kernel_rooflines(body, reps):
     """Per-launch time of each entry point: a graph of one launch per layer of that kernel
     alone (distinct tensors, as in the sweep), replayed `reps` times, timed with HIP events
@@ -605,6 +639,7 @@ def main():
     api = run_api_variant(dev, max(args.steps // 3, 5))
     attn = None if args.no_attention else run_attention(dev, max(args.steps // 3, 5))
     swi = run_swiglu(dev, max(args.steps // 3, 5))
+    lora = run_lora_dropout(dev, max(args.steps // 3, 5))
 
     cpu = None
     if not args.no_cpu:
@@ -634,6 +669,7 @@ def main():
         "api_variant": api,
         "attention": attn,
         "swiglu": swi,
+        "lora_dropout": lora,
     }
     print(json.dumps(out), flush=True)
     return 0
