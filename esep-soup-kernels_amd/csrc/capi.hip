@@ -7,6 +7,7 @@
 #include "attention.hpp"
 #include "dropout.hpp"
 #include "esep_body.h"
+#include "nf4.hpp"
 #include "rmsnorm.hpp"
 #include "rope.hpp"
 #include "swiglu.hpp"
@@ -553,6 +554,25 @@ int esep_lora_dropout_bwd(const void* x, const void* g, const int64_t* key, void
                                                 static_cast<hipStream_t>(stream), &sup);
   if (!sup) return fail(ESEP_EINVAL, "lora_dropout_bwd: unsupported dtype");
   return e == hipSuccess ? 0 : hip_fail(e, "lora_dropout_bwd launch");
+}
+
+int esep_nf4_dequant(const void* packed, const uint8_t* absmax, const float* absmax2,
+                     const float* code2, const float* offset, const float* nf4, void* out,
+                     int out_dt, int64_t n_blocks, void* stream) {
+  g_err[0] = 0;
+  if (!float_dt(out_dt)) return fail(ESEP_EINVAL, "nf4_dequant: bad output dtype code %d", out_dt);
+  if (n_blocks < 0) return fail(ESEP_ESHAPE, "nf4_dequant: n_blocks=%lld < 0", (long long)n_blocks);
+  if (n_blocks == 0) return 0;
+  if (packed == nullptr || absmax == nullptr || absmax2 == nullptr || code2 == nullptr ||
+      offset == nullptr || nf4 == nullptr || out == nullptr)
+    return fail(ESEP_EINVAL, "nf4_dequant: every pointer is required");
+  if ((reinterpret_cast<uintptr_t>(packed) & 7) || !aligned16(out))
+    return fail(ESEP_EALIGN, "nf4_dequant: packed needs 8-byte and out 16-byte alignment");
+  esep::Nf4Args a{packed, absmax, absmax2, code2, offset, nf4, out, n_blocks};
+  bool sup = false;
+  const hipError_t e = esep::launch_nf4_dequant(a, out_dt, static_cast<hipStream_t>(stream), &sup);
+  if (!sup) return fail(ESEP_EINVAL, "nf4_dequant: unsupported output dtype");
+  return e == hipSuccess ? 0 : hip_fail(e, "nf4_dequant launch");
 }
 
 }  // extern "C"

@@ -47,6 +47,7 @@ SIGNATURES = {
     "esep_attn_bwd_workspace": (_i64, [_i64, _i32, _i32, _i32]),
     "esep_swiglu_fwd": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp]),
     "esep_lora_dropout_fwd": (_i32, [_vp, _vp, _vp, _i64, _f32, _i32, _vp]),
+    "esep_nf4_dequant": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _vp]),
     "esep_lora_dropout_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _f32, _i32, _i32, _vp]),
     "esep_swiglu_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _vp]),
     "esep_attn_bwd": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp,
@@ -423,4 +424,25 @@ def lora_dropout_bwd(x, g, key, xd, dx, p, accumulate=False, name="_lora_dropout
                                      _p(_flat(xd, "xd")), _p(_flat(dx, "dx")), n, float(p),
                                      int(bool(accumulate)), dtype_code(x.dtype), _stream(dev))
     _check(rc, "esep_lora_dropout_bwd")
+    _record(name)
+
+
+def nf4_dequant(packed, absmax, absmax2, code2, offset, nf4, out, name="_nf4_dequant"):
+    """out = NF4 double-quant dequantization (esep_nf4_dequant). packed uint8 (n_blocks * 32
+    bytes, any contiguous view), absmax uint8 [n_blocks], absmax2 / code2 / offset / nf4 fp32
+    device tensors, out: n_blocks * 64 contiguous elements (fp16 / bf16 / fp32)."""
+    dev = _dev(packed, absmax, absmax2, code2, offset, nf4, out)
+    nb = absmax.numel()
+    if packed.dtype != torch.uint8 or packed.numel() != nb * 32 or absmax.dtype != torch.uint8:
+        raise EsepError("packed must hold n_blocks * 32 uint8 and absmax n_blocks uint8")
+    for t, nm in ((absmax2, "absmax2"), (code2, "code2"), (offset, "offset"), (nf4, "nf4")):
+        if t.dtype != torch.float32 or not t.is_contiguous():
+            raise EsepError(f"{nm} must be a contiguous fp32 tensor")
+    if absmax2.numel() < (nb + 255) // 256 or code2.numel() < 256 or nf4.numel() < 16 or offset.numel() < 1:
+        raise EsepError("nf4 tables too small")
+    if out.numel() != nb * 64 or not out.is_contiguous():
+        raise EsepError("out must be n_blocks * 64 contiguous elements")
+    rc = lib().esep_nf4_dequant(_p(packed), _p(absmax.contiguous()), _p(absmax2), _p(code2),
+                                _p(offset), _p(nf4), _p(out), dtype_code(out.dtype), nb, _stream(dev))
+    _check(rc, "esep_nf4_dequant")
     _record(name)

@@ -248,6 +248,21 @@ int esep_lora_dropout_fwd(const void* x, const int64_t* key, void* xd, int64_t n
 int esep_lora_dropout_bwd(const void* x, const void* g, const int64_t* key, void* xd, void* dx,
                           int64_t n, float p, int accumulate, int dt, void* stream);
 
+/*
+ * NF4 double-quant weight dequantization (QLoRA / bitsandbytes Linear4bit format). Replaces the
+ * reference's Triton launch at solution/nf4/dequant.py:85-89 (dequantize_nf4; kernel math
+ * dequant.py:35-57):
+ *   scale[b] = (code2[absmax[b]] * absmax2[b / 256]) + *offset     each op rounded in fp32
+ *   out[e]   = nf4[nibble(e)] * scale[e / 64]                       rounded to out_dt once
+ * packed: n_blocks * 32 bytes (byte i: element 2i in the high nibble, 2i + 1 in the low one),
+ * 8-byte aligned; absmax uint8 [n_blocks]; absmax2 fp32 [ceil(n_blocks / 256)]; code2 fp32 [256];
+ * offset: one fp32 in device memory; nf4 fp32 [16]; out: n_blocks * 64 elements of out_dt
+ * (fp16 as the reference, also bf16 / fp32), 16-byte aligned.
+ */
+int esep_nf4_dequant(const void* packed, const uint8_t* absmax, const float* absmax2,
+                     const float* code2, const float* offset, const float* nf4, void* out,
+                     int out_dt, int64_t n_blocks, void* stream);
+
 #ifdef __cplusplus
 }
 #endif
