@@ -485,6 +485,43 @@ def run_lora_dropout(dev, reps, n_sets=4):
                         "input of config 4: T=8192 x 1536, bf16, p=0.05", **out}
 
 
+def run_nf4(dev, reps):
+    """NF4 dequantization of the four Qwen2.5-1.5B projection shapes of one layer (q, k, v, o,
+    gate, up, down: 1536x1536 x2, 256x1536 x2, 8960x1536 x2, 1536x8960) to fp16: per element
+    0.5 byte of codes in, 2 bytes out, plus one scale byte per 64 (algorithmic bytes)."""
+    import torch
+
+    from solution.body import _hip
+
+    shapes = [(1536, 1536), (256, 1536), (256, 1536), (1536, 1536), (8960, 1536), (8960, 1536),
+              (1536, 8960)]
+    g = torch.Generator(device=dev).manual_seed(19)
+    tabs = dict(code2=torch.sort(torch.randn(256, generator=g, device=dev))[0],
+                offset=torch.tensor([0.01], device=dev),
+                nf4=torch.linspace(-1, 1, 16, device=dev))
+    ws = []
+    for n, k in shapes:
+        nb = n * k // 64
+        ws.append(dict(packed=torch.randint(0, 256, (nb * 32,), generator=g, device=dev, dtype=torch.uint8),
+                       absmax=torch.randint(0, 256, (nb,), generator=g, device=dev, dtype=torch.uint8),
+                       absmax2=torch.rand((nb + 255) // 256, generator=g, device=dev),
+                       out=torch.empty(n, k, device=dev, dtype=torch.float16)))
+    elems = sum(n * k for n, k in shapes)
+    nbytes = elems // 2 + elems // 64 + 2 * elems
+    fn = lambda: [_hip.nf4_dequant(w["packed"], w["absmax"], w["absmax2"], tabs["code2"], tabs["offset"],
+                                   tabs["nf4"], w["out"]) for w in ws]
+    gr = capture(fn)
+    time_graph(gr, 2)
+    ms, _ = time_graph(gr, reps)
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"nf4 dequant (one layer, 7 weights): {ms * 1e3:.1f} us, {gbs:.0f} GB/s = {gbs / PEAK_GBS:.1%} of peak")
+    del gr, ws
+    torch.cuda.empty_cache()
+    return {"workload": "NF4 double-quant dequantization to fp16 of one Qwen2.5-1.5B layer's seven "
+                        "projection weights (7 launches)", "us": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+            "frac": round(gbs / PEAK_GBS, 4), "bytes": nbytes}
+
+
 def kernel_rooflines(body, reps):
     """Per-launch time of each entry point: a graph of one launch per layer of that kernel
     alone (distinct tensors, as in the sweep), replayed `reps` times, timed with HIP events
@@ -640,6 +677,7 @@ def main():
     attn = None if args.no_attention else run_attention(dev, max(args.steps // 3, 5))
     swi = run_swiglu(dev, max(args.steps // 3, 5))
     lora = run_lora_dropout(dev, max(args.steps // 3, 5))
+    nf4 = run_nf4(dev, max(args.steps // 3, 5))
 
     cpu = None
     if not args.no_cpu:
@@ -670,6 +708,7 @@ def main():
         "attention": attn,
         "swiglu": swi,
         "lora_dropout": lora,
+        "nf4_dequant": nf4,
     }
     print(json.dumps(out), flush=True)
     return 0
