@@ -7,6 +7,7 @@
 #include "attention.hpp"
 #include "dropout.hpp"
 #include "esep_body.h"
+#include "head.hpp"
 #include "nf4.hpp"
 #include "rmsnorm.hpp"
 #include "rope.hpp"
@@ -573,6 +574,34 @@ int esep_nf4_dequant(const void* packed, const uint8_t* absmax, const float* abs
   const hipError_t e = esep::launch_nf4_dequant(a, out_dt, static_cast<hipStream_t>(stream), &sup);
   if (!sup) return fail(ESEP_EINVAL, "nf4_dequant: unsupported output dtype");
   return e == hipSuccess ? 0 : hip_fail(e, "nf4_dequant launch");
+}
+
+int esep_head_row_softmax(void* z, int64_t ld, const int64_t* target, const float* cew,
+                          float* lse, float* tlogit, float* ent, int32_t* amax, int64_t rows,
+                          int64_t V, int write_g, float g_scale, int dt, void* stream) {
+  g_err[0] = 0;
+  if (dt != ESEP_F16 && dt != ESEP_BF16)
+    return fail(ESEP_EINVAL, "head_row_softmax: logits must be fp16 or bf16 (dtype code %d)", dt);
+  if (rows < 0 || rows > 0x7fffffffLL)
+    return fail(ESEP_ESHAPE, "head_row_softmax: rows=%lld out of range", (long long)rows);
+  if (V < 1 || V > (1LL << 30))
+    return fail(ESEP_ESHAPE, "head_row_softmax: V=%lld outside [1, 2^30]", (long long)V);
+  if (ld < V) return fail(ESEP_ESHAPE, "head_row_softmax: ld=%lld < V=%lld", (long long)ld,
+                          (long long)V);
+  if (rows == 0) return 0;
+  if (z == nullptr || target == nullptr || lse == nullptr || tlogit == nullptr || ent == nullptr ||
+      amax == nullptr || (write_g && cew == nullptr))
+    return fail(ESEP_EINVAL, "head_row_softmax: z, target, lse, tlogit, ent, amax (and cew with "
+                             "write_g) are required");
+  if (reinterpret_cast<uintptr_t>(z) & 1)
+    return fail(ESEP_EALIGN, "head_row_softmax: z must be 2-byte aligned");
+  const bool vec = aligned16(z) && (ld & 7) == 0 && (V & 7) == 0;
+  esep::HeadArgs a{z, target, cew, lse, tlogit, ent, amax, rows, ld, V, g_scale, write_g ? 1 : 0};
+  bool sup = false;
+  const hipError_t e =
+      esep::launch_head_row(a, dt, vec, static_cast<hipStream_t>(stream), &sup);
+  if (!sup) return fail(ESEP_EINVAL, "head_row_softmax: unsupported dtype");
+  return e == hipSuccess ? 0 : hip_fail(e, "head_row_softmax launch");
 }
 
 }  // extern "C"

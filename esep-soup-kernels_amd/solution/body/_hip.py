@@ -48,6 +48,8 @@ SIGNATURES = {
     "esep_swiglu_fwd": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp]),
     "esep_lora_dropout_fwd": (_i32, [_vp, _vp, _vp, _i64, _f32, _i32, _vp]),
     "esep_nf4_dequant": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _vp]),
+    "esep_head_row_softmax": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32,
+                                     _f32, _i32, _vp]),
     "esep_lora_dropout_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _f32, _i32, _i32, _vp]),
     "esep_swiglu_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _vp]),
     "esep_attn_bwd": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp,
@@ -445,4 +447,25 @@ def nf4_dequant(packed, absmax, absmax2, code2, offset, nf4, out, name="_nf4_deq
     rc = lib().esep_nf4_dequant(_p(packed), _p(absmax.contiguous()), _p(absmax2), _p(code2),
                                 _p(offset), _p(nf4), _p(out), dtype_code(out.dtype), nb, _stream(dev))
     _check(rc, "esep_nf4_dequant")
+    _record(name)
+
+
+def head_row_softmax(z, target, cew, lse, tlogit, ent, amax, write_g, g_scale,
+                     name="head_row_softmax_kernel"):
+    """Softmax statistics of the logits chunk z [rows, V] (fp16 / bf16, unit column stride) and,
+    with write_g, g = (softmax - onehot) * g_scale written over the rows whose cew is != 0
+    (esep_head_row_softmax). target int64 [rows]; cew fp32 [rows]; lse / tlogit / ent fp32 and
+    amax int32 outputs of [rows]."""
+    dev = _dev(z, target, cew, lse, tlogit, ent, amax)
+    rows, V = z.shape
+    ld = _rows_ld(z, V)
+    for t, dt, nm in ((target, torch.int64, "target"), (cew, torch.float32, "cew"),
+                      (lse, torch.float32, "lse"), (tlogit, torch.float32, "tlogit"),
+                      (ent, torch.float32, "ent"), (amax, torch.int32, "amax")):
+        if t.dtype != dt or t.numel() != rows or (rows > 1 and t.stride(0) != 1):
+            raise EsepError(f"{nm} must be a contiguous {dt} tensor of {rows} elements")
+    rc = lib().esep_head_row_softmax(_p(z), ld, _p(target), _p(cew), _p(lse), _p(tlogit), _p(ent),
+                                     _p(amax), rows, V, 1 if write_g else 0, float(g_scale),
+                                     dtype_code(z.dtype), _stream(dev))
+    _check(rc, "esep_head_row_softmax")
     _record(name)

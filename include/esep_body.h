@@ -263,6 +263,24 @@ int esep_nf4_dequant(const void* packed, const uint8_t* absmax, const float* abs
                      const float* code2, const float* offset, const float* nf4, void* out,
                      int out_dt, int64_t n_blocks, void* stream);
 
+/*
+ * Fused LM head: softmax statistics and dlogits of one logits chunk. Replaces the reference's
+ * Triton launch at solution/head/op.py:79-84 (_run; kernel head_row_softmax_kernel,
+ * solution/head/kernels.py:37-93). For each row r of z ([rows, V] of dt, row stride ld):
+ *   lse[r]    = log sum_v exp(z[r,v])                 (fp32, online over the row)
+ *   ent[r]    = -sum_v p_v log p_v, p = softmax(z[r])  (as log S - T / S, no cancellation)
+ *   amax[r]   = first v with z[r,v] = max_v z[r,v]     (int32)
+ *   tlogit[r] = z[r, target[r]], or 0 when target[r] is outside [0, V)
+ * and, when write_g and cew[r] != 0, z[r] is overwritten in place with
+ *   g[r,v] = (p_v - [v == target[r]]) * g_scale        (rounded to dt)
+ * dt: fp16 (the reference's) or bf16. target int64 [rows]; cew fp32 [rows] (read only when
+ * write_g); 1 <= V <= 2^30; ld >= V. z, lse, tlogit, ent, amax may be any device pointers;
+ * 16-byte aligned z with ld and V multiples of 8 takes the 16-byte-load path.
+ */
+int esep_head_row_softmax(void* z, int64_t ld, const int64_t* target, const float* cew,
+                          float* lse, float* tlogit, float* ent, int32_t* amax, int64_t rows,
+                          int64_t V, int write_g, float g_scale, int dt, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -166,3 +166,24 @@ def test_attention_workspace_size():
     # 8192 tokens, 12/2 heads: 32 x 2 blocks, split over all 6 query heads of a kv head
     assert ws(8192, 12, 2, 128) == 12 * 8192 + 2 * 6 * 8192 * 2 * 128
     assert ws(3, 1, 1, 64) == 4  # delta rounded up to a multiple of 4 floats
+
+
+def test_head_row_softmax_validation():
+    """esep_head_row_softmax rejects bad arguments before launching anything."""
+    lib = _hip.lib()
+
+    def call(**kw):
+        a = dict(z=16, ld=1024, target=16, cew=16, lse=16, tlogit=16, ent=16, amax=16, rows=4,
+                 V=1000, write_g=1, g_scale=1024.0, dt=1, stream=None)
+        a.update(kw)
+        return lib.esep_head_row_softmax(*a.values())
+
+    assert call(dt=0) == -1 and b"fp16 or bf16" in lib.esep_last_error()
+    assert call(dt=4) == -1
+    assert call(V=0) == -2 and call(V=(1 << 30) + 1) == -2
+    assert call(ld=999) == -2 and b"ld" in lib.esep_last_error()
+    assert call(rows=-1) == -2
+    assert call(z=None) == -1 and call(amax=None) == -1
+    assert call(cew=None) == -1  # the CE weights decide which rows get g
+    assert call(z=17) == -3
+    assert call(rows=0) == 0  # nothing to do, nothing launched
