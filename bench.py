@@ -522,6 +522,71 @@ def run_nf4(dev, reps):
             "frac": round(gbs / PEAK_GBS, 4), "bytes": nbytes}
 
 
+def run_lm_head(dev, reps):
+    """The fused LM head (solution.head.fused_linear_ce) on the Qwen2.5-1.5B head: N = 8192 rows
+    (config 4's tokens), H = 1536, V = 151936, fp16 weight and hidden states, every 7th row
+    ignored. Reported: the row kernel esep_head_row_softmax alone on one 4096-row chunk
+    (statistics only: one read of the chunk; with g on every row: two reads and one write, the
+    algorithmic bytes), and the whole op (forward with the dX precompute, then backward) at the
+    default chunk and at the reference's 256-row chunk, with its two GEMMs' FLOP rate."""
+    import torch
+
+    from solution.body import _hip
+    from solution.head import op as head
+
+    N, H, V, rows = CFG4["B"] * CFG4["S"], CFG4["H"], head.VOCAB, 4096
+    g = torch.Generator(device=dev).manual_seed(23)
+    out = {}
+    z = (torch.randn(rows, V, generator=g, device=dev) * 3).to(torch.float16)
+    tgt = torch.randint(0, V, (rows,), generator=g, device=dev)
+    cew = torch.ones(rows, device=dev)
+    st = [torch.empty(rows, device=dev) for _ in range(3)] + [torch.empty(rows, device=dev, dtype=torch.int32)]
+    for kind, wg, nbytes in (("row_stats", False, rows * V * 2), ("row_stats_g", True, 3 * rows * V * 2)):
+        gr = capture(lambda: _hip.head_row_softmax(z, tgt, cew, *st, wg, head.G_SCALE))
+        time_graph(gr, 2)
+        ms, _ = time_graph(gr, reps)
+        gbs = nbytes / (ms * 1e-3) / 1e9
+        out[kind] = {"us": round(ms * 1e3, 2), "GB/s": round(gbs, 1), "frac": round(gbs / PEAK_GBS, 4),
+                     "bytes": nbytes, "rows": rows}
+        log(f"lm head {kind} ({rows} x {V}): {ms * 1e3:.1f} us, {gbs:.0f} GB/s = {gbs / PEAK_GBS:.1%} of peak")
+        del gr
+    del z, st
+    torch.cuda.empty_cache()
+    w = (torch.randn(V, H, generator=g, device=dev) * 0.02).to(torch.float16)
+    x = torch.randn(N, H, generator=g, device=dev).to(torch.float16)
+    target = torch.randint(0, V, (N,), generator=g, device=dev)
+    target[::7] = -100
+    ce_w = torch.full((N,), 1.0 / N, device=dev)
+    flops = 2 * (2 * N * H * V) * 6 / 7 + 2 * N * H * V / 7  # dX GEMM on the weighted rows only
+
+    def step(chunk):
+        xg = x.detach().requires_grad_(True)
+        loss, _ = head.fused_linear_ce(xg, w, target, ce_w, chunk_rows=chunk)
+        loss.backward()
+
+    for key, chunk in (("op", head.CHUNK_ROWS), ("op_chunk256_reference_setting", 256)):
+        for _ in range(2):
+            step(chunk)
+        torch.cuda.synchronize()
+        n = max(reps // 4, 3)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(n):
+            step(chunk)
+        e1.record()
+        torch.cuda.synchronize()
+        ms = e0.elapsed_time(e1) / n
+        tfs = flops / (ms * 1e-3) / 1e12
+        out[key] = {"ms": round(ms, 3), "chunk_rows": chunk, "TFLOP/s": round(tfs, 1),
+                    "frac_mfma_fp16": round(tfs / PEAK_BF16_TFLOPS, 4)}
+        log(f"lm head {key} (chunk {chunk}): {ms:.3f} ms, {tfs:.0f} TFLOP/s of GEMM work")
+    del w, x
+    torch.cuda.empty_cache()
+    return {"workload": f"fused linear + cross-entropy over the Qwen2.5-1.5B head: N={N}, H={H}, "
+                        f"V={V}, fp16, forward (stats + dX) and backward; row kernel on one "
+                        f"{rows}-row chunk", "gemm_flops": int(flops), **out}
+
+
 def kernel_rooflines(body, reps):
     """Per-launch time of each entry point: a graph of one launch per layer of that kernel
     alone (distinct tensors, as in the sweep), replayed `reps` times, timed with HIP events
@@ -601,6 +666,7 @@ def main():
     ap.add_argument("--kernel-reps", type=int, default=20)
     ap.add_argument("--no-config5", action="store_true", help="skip the config 5 stress line")
     ap.add_argument("--no-attention", action="store_true", help="skip the attention measurement")
+    ap.add_argument("--no-lm-head", action="store_true", help="skip the fused LM head measurement")
     ap.add_argument("--pmc-kernel", choices=["rmsnorm_fwd", "rmsnorm_bwd", "rope_fwd", "rope_bwd"],
                     help="counter-collection run: a calibration copy of 256 MiB (read 256 MiB, "
                          "write 256 MiB) three times, then one launch per layer of this kernel "
@@ -678,6 +744,7 @@ def main():
     swi = run_swiglu(dev, max(args.steps // 3, 5))
     lora = run_lora_dropout(dev, max(args.steps // 3, 5))
     nf4 = run_nf4(dev, max(args.steps // 3, 5))
+    lmh = None if args.no_lm_head else run_lm_head(dev, max(args.steps // 3, 5))
 
     cpu = None
     if not args.no_cpu:
@@ -709,6 +776,7 @@ def main():
         "swiglu": swi,
         "lora_dropout": lora,
         "nf4_dequant": nf4,
+        "lm_head": lmh,
     }
     print(json.dumps(out), flush=True)
     return 0
