@@ -93,6 +93,10 @@ struct Mfma<_Float16> {
   }
 };
 
+// 2^x on the hardware's v_exp_f32 alone (no denormal-range scaling: results below 2^-126 flush
+// to 0, far below what a probability contributes next to the sums they enter).
+__device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
+
 template <typename V>
 __device__ __forceinline__ V ld16(const void* p) {
   return __builtin_bit_cast(V, *reinterpret_cast<const uint4*>(p));

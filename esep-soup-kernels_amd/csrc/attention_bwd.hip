@@ -105,11 +105,18 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq(const AttnBwdArgs b)
         s = Mfma<T>::run(ld16<V8>(krow + 16 * c), qb[c], s);
         dp = Mfma<T>::run(ld16<V8>(vrow + 16 * c), db[c], dp);
       }
+      // the causal mask only bites on the half-tiles that reach past the wave's first query
+      if (kt + 32 * sb + 31 > qw0) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int kj = kt + 32 * sb + 8 * (i / 4) + 4 * hi + (i % 4);
+          if (kj > qi) s[i] = -INFINITY;
+        }
+      }
       V8 dsb[2];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const int kj = kt + 32 * sb + 8 * (i / 4) + 4 * hi + (i % 4);
-        const float p = kj <= qi ? exp2f(s[i] * a.scale_log2 - lse2) : 0.f;
+        const float p = exp2_fast(fmaf(s[i], a.scale_log2, -lse2));
         dsb[i / 8][i % 8] = (T)(p * (dp[i] - delta));
       }
       // dQ^T += K^T dS^T, keys in the permuted order of dsb
@@ -193,7 +200,8 @@ __global__ __launch_bounds__(64 * dkdv_waves<D>(), 2) void k_attn_bwd_dkdv(const
   __shared__ __align__(16) T ds_[BQ * RP];  // dO row-major (A operand of dP)
   __shared__ __align__(16) T qt_[D * CP];   // Q^T (A operand of dK^T)
   __shared__ __align__(16) T dt_[D * CP];   // dO^T (A operand of dV^T)
-  __shared__ float lse_s[BQ], del_s[BQ];
+  __shared__ __align__(16) float lse_s[BQ];
+  __shared__ __align__(16) float del_s[BQ];
   __shared__ __align__(16) T vsm[BK * RP];  // this block's V rows (B operands of dP)
 
   const int seq = blockIdx.z;
@@ -272,15 +280,30 @@ __global__ __launch_bounds__(64 * dkdv_waves<D>(), 2) void k_attn_bwd_dkdv(const
         s = Mfma<T>::run(ld16<V8>(qrow + 16 * c), kb[c], s);
         dp = Mfma<T>::run(ld16<V8>(drow + 16 * c), ld16<V8>(vlds + 16 * c), dp);
       }
-      // s[i] is S[q][kj] for query row r = 32 qh + 8 (i / 4) + 4 hi + i % 4 of the tile
+      // s[i] is S[q][kj] for query row r = 32 qh + 8 (i / 4) + 4 hi + i % 4 of the tile. Rows
+      // past the sequence end have Q = dO = 0 (staged as zeros), so they add nothing to dK or
+      // dV whatever their p; only the causal mask needs applying, and only on the half-tiles
+      // whose first query precedes the wave's last key.
+      if (qt + 32 * qh < kw0 + 31) {
+#pragma unroll
+        for (int i = 0; i < 16; ++i) {
+          const int t = qt + 32 * qh + 8 * (i / 4) + 4 * hi + (i % 4);
+          if (t < kj) s[i] = -INFINITY;
+        }
+      }
       V8 pb[2], sb_[2];
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int r = 32 * qh + 8 * (i / 4) + 4 * hi + (i % 4);
-        const int t = qt + r;
-        const float p = (kj <= t && t < end) ? exp2f(s[i] * a.scale_log2 - lse_s[r]) : 0.f;
-        pb[i / 8][i % 8] = (T)p;
-        sb_[i / 8][i % 8] = (T)(p * (dp[i] - del_s[r]));
+      for (int j = 0; j < 4; ++j) {
+        const float4 l4 = *reinterpret_cast<const float4*>(&lse_s[32 * qh + 8 * j + 4 * hi]);
+        const float4 d4 = *reinterpret_cast<const float4*>(&del_s[32 * qh + 8 * j + 4 * hi]);
+        const float lr[4] = {l4.x, l4.y, l4.z, l4.w}, dr[4] = {d4.x, d4.y, d4.z, d4.w};
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * j + e;
+          const float p = exp2_fast(fmaf(s[i], a.scale_log2, -lr[e]));
+          pb[i / 8][i % 8] = (T)p;
+          sb_[i / 8][i % 8] = (T)(p * (dp[i] - dr[e]));
+        }
       }
       // dV^T += dO^T P and dK^T += Q^T dS, queries in the permuted order of pb / sb_
 #pragma unroll

@@ -65,35 +65,46 @@ __global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd(const AttnArgs a) 
       const T* krow = &ks[(32 * sb + lq) * KP + 8 * hi];
 #pragma unroll
       for (int c = 0; c < D / 16; ++c) acc = Mfma<T>::run(ld16<V8>(krow + 16 * c), qb[c], acc);
-      float sc[16];
-      float mx = -INFINITY;
+      // the causal mask only bites on the half-tiles that reach past the wave's first query
+      if (kt + 32 * sb + 31 > qw0) {
 #pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const int kj = kt + 32 * sb + 8 * (i / 4) + 4 * hi + (i % 4);
-        sc[i] = kj <= qi ? acc[i] * a.scale_log2 : -INFINITY;
-        mx = fmaxf(mx, sc[i]);
+        for (int i = 0; i < 16; ++i) {
+          const int kj = kt + 32 * sb + 8 * (i / 4) + 4 * hi + (i % 4);
+          if (kj > qi) acc[i] = -INFINITY;
+        }
       }
-      // online softmax (base 2): running max m and sum l per query
-      mx = fmaxf(mx, __shfl_xor(mx, 32));
-      const float mnew = fmaxf(m, mx);
-      const float mu = mnew == -INFINITY ? 0.f : mnew;
-      const float alpha = exp2f(m - mu);
+      float mx = acc[0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) mx = fmaxf(mx, acc[i]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32)) * a.scale_log2;
+      // Online softmax (base 2) with a lazy reference: the lane's m moves only when the half's
+      // maximum exceeds it by more than 8, so p <= 2^8 (exact in bf16 / fp16 relative terms)
+      // and O, l are rescaled only in the rare half-tiles where some lane's m moved.
+      const bool grow = mx > m + 8.f;
+      float alpha = 1.f;
+      if (grow) {
+        alpha = exp2_fast(m - mx);  // m = -inf on the first half: alpha = 0, O and l are 0
+        m = mx;
+      }
+      const float nm = m == -INFINITY ? 0.f : -m;  // a lane with no visible key yet: p = 0
       float ps = 0.f;
       V8 pb[2];
 #pragma unroll
       for (int i = 0; i < 16; ++i) {
-        const float p = exp2f(sc[i] - mu);
+        const float p = exp2_fast(fmaf(acc[i], a.scale_log2, nm));
         ps += p;
         pb[i / 8][i % 8] = (T)p;
       }
       ps += __shfl_xor(ps, 32);
-      l = l * alpha + ps;
-      m = mnew;
+      l = fmaf(l, alpha, ps);
+      if (__any(grow)) {
+#pragma unroll
+        for (int md = 0; md < D / 32; ++md) oacc[md] *= alpha;
+      }
       // O^T += V^T P^T over the 32 keys, contraction in the permuted key order of pb: element e
       // of chunk c2 is key 32 sb + 16 c2 + 8 (e / 4) + 4 hi + e % 4.
 #pragma unroll
       for (int md = 0; md < D / 32; ++md) {
-        oacc[md] *= alpha;
         const T* vrow = &vt[(32 * md + lq) * VP + 4 * hi];
 #pragma unroll
         for (int c2 = 0; c2 < 2; ++c2) {
