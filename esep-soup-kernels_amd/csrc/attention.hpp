@@ -93,6 +93,12 @@ struct Mfma<_Float16> {
   }
 };
 
+// Padding (elements) of the transposed LDS tiles (V^T, K^T, Q^T, dO^T: 64 columns): a pitch of
+// 68 bf16 = 34 dwords puts the 32 rows an 8-byte operand read touches on 32 distinct bank pairs
+// (34 r mod 64 covers every even bank once); +8 (36 dwords) left 2-way conflicts and measured
+// 6% slower in the backward.
+constexpr int kTPad = 4;
+
 // 2^x on the hardware's v_exp_f32 alone (no denormal-range scaling: results below 2^-126 flush
 // to 0, far below what a probability contributes next to the sums they enter).
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -119,39 +125,91 @@ __device__ __forceinline__ void seq_bounds(const int32_t* cu, int s, int64_t T, 
   *end = c1 < *start ? *start : (c1 > tt ? tt : c1);
 }
 
-// Stage a [rows x D] tile (token rows r0 .. r0 + rows - 1 below rend; the rest reads as 0)
-// into LDS row-major with pitch P elements.
-template <typename T, int D, int ROWS, int P, int NT = kAttnThreads>
-__device__ __forceinline__ void stage_rows(T* dst, const T* base, int64_t rs, int r0, int rend,
-                                           int tid) {
-  for (int idx = tid; idx < ROWS * (D / 8); idx += NT) {
-    const int r = idx % ROWS, dc = idx / ROWS;
-    uint4 val = make_uint4(0, 0, 0, 0);
-    if (r0 + r < rend) val = *reinterpret_cast<const uint4*>(base + (int64_t)(r0 + r) * rs + 8 * dc);
-    *reinterpret_cast<uint4*>(&dst[r * P + 8 * dc]) = val;
-  }
-}
+// A [ROWS x D] tile (token rows r0 .. r0 + ROWS - 1 below rend; the rest reads as 0) moved
+// through registers into LDS. load() issues every global read of the thread before any is
+// used (one memory round trip per tile, not one per chunk); the tile can be loaded before the
+// barrier that frees its LDS buffer and stored after it.
+//   rows():  thread tid holds chunks idx = tid + NT j: row idx % ROWS, 8-column chunk
+//            idx / ROWS; store_rows() writes them row-major with pitch P.
+template <typename T, int D, int ROWS, int NT = kAttnThreads>
+struct TileRows {
+  static constexpr int N = ROWS * (D / 8) / NT;
+  static_assert(N >= 1 && ROWS * (D / 8) % NT == 0, "tile / block mismatch");
+  uint4 r[N];
 
-// Stage the same tile transposed, [D x ROWS] with pitch P: a thread takes rows (2p, 2p + 1) of
-// one 8-column chunk and writes 8 dwords (one per column), each holding the two rows' values.
-template <typename T, int D, int ROWS, int P, int NT = kAttnThreads>
-__device__ __forceinline__ void stage_cols(T* dst, const T* base, int64_t rs, int r0, int rend,
-                                           int tid) {
-  for (int idx = tid; idx < (ROWS / 2) * (D / 8); idx += NT) {
-    const int p = idx % (ROWS / 2), dc = idx / (ROWS / 2);
-    const int r = r0 + 2 * p;
-    uint4 v0 = make_uint4(0, 0, 0, 0), v1 = make_uint4(0, 0, 0, 0);
-    if (r < rend) v0 = *reinterpret_cast<const uint4*>(base + (int64_t)r * rs + 8 * dc);
-    if (r + 1 < rend) v1 = *reinterpret_cast<const uint4*>(base + (int64_t)(r + 1) * rs + 8 * dc);
-    const uint32_t w0[4] = {v0.x, v0.y, v0.z, v0.w}, w1[4] = {v1.x, v1.y, v1.z, v1.w};
+  __device__ __forceinline__ void load(const T* base, int64_t rs, int r0, int rend, int tid) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) {
-      const uint32_t lo = (w0[e / 2] >> (16 * (e % 2))) & 0xffffu;
-      const uint32_t up = (w1[e / 2] >> (16 * (e % 2))) & 0xffffu;
-      *reinterpret_cast<uint32_t*>(&dst[(8 * dc + e) * P + 2 * p]) = lo | (up << 16);
+    for (int j = 0; j < N; ++j) {
+      const int idx = tid + NT * j;
+      const int row = r0 + idx % ROWS, dc = idx / ROWS;
+      r[j] = row < rend ? *reinterpret_cast<const uint4*>(base + (int64_t)row * rs + 8 * dc)
+                        : make_uint4(0, 0, 0, 0);
     }
   }
-}
+
+  template <int P>
+  __device__ __forceinline__ void store(T* dst, int tid) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = tid + NT * j;
+      *reinterpret_cast<uint4*>(&dst[(idx % ROWS) * P + 8 * (idx / ROWS)]) = r[j];
+    }
+  }
+};
+
+// A [ROWS x D] tile in row pairs for a transposed copy: thread tid takes pairs idx = tid + NT j,
+// rows (2p, 2p + 1) of 8-column chunk dc (p = idx % (ROWS / 2), dc = idx / (ROWS / 2)).
+// store_cols() writes the tile transposed ([D x ROWS], pitch CP: one dword per column holding
+// the two rows' values); store_both() also writes it row-major (pitch RP), so each global chunk
+// is read once for both copies.
+template <typename T, int D, int ROWS, int NT = kAttnThreads>
+struct TilePairs {
+  static constexpr int N = (ROWS / 2) * (D / 8) / NT;
+  static_assert(N >= 1 && (ROWS / 2) * (D / 8) % NT == 0, "tile / block mismatch");
+  uint4 r0[N], r1[N];
+
+  __device__ __forceinline__ void load(const T* base, int64_t rs, int t0, int tend, int tid) {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = tid + NT * j;
+      const int p = idx % (ROWS / 2), dc = idx / (ROWS / 2);
+      const int t = t0 + 2 * p;
+      r0[j] = t < tend ? *reinterpret_cast<const uint4*>(base + (int64_t)t * rs + 8 * dc)
+                       : make_uint4(0, 0, 0, 0);
+      r1[j] = t + 1 < tend ? *reinterpret_cast<const uint4*>(base + (int64_t)(t + 1) * rs + 8 * dc)
+                           : make_uint4(0, 0, 0, 0);
+    }
+  }
+
+  template <int CP>
+  __device__ __forceinline__ void store_cols(T* cols, int tid) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = tid + NT * j;
+      const int p = idx % (ROWS / 2), dc = idx / (ROWS / 2);
+      const uint32_t w0[4] = {r0[j].x, r0[j].y, r0[j].z, r0[j].w};
+      const uint32_t w1[4] = {r1[j].x, r1[j].y, r1[j].z, r1[j].w};
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t lo = (w0[e / 2] >> (16 * (e % 2))) & 0xffffu;
+        const uint32_t up = (w1[e / 2] >> (16 * (e % 2))) & 0xffffu;
+        *reinterpret_cast<uint32_t*>(&cols[(8 * dc + e) * CP + 2 * p]) = lo | (up << 16);
+      }
+    }
+  }
+
+  template <int RP, int CP>
+  __device__ __forceinline__ void store_both(T* rows, T* cols, int tid) const {
+#pragma unroll
+    for (int j = 0; j < N; ++j) {
+      const int idx = tid + NT * j;
+      const int p = idx % (ROWS / 2), dc = idx / (ROWS / 2);
+      *reinterpret_cast<uint4*>(&rows[(2 * p) * RP + 8 * dc]) = r0[j];
+      *reinterpret_cast<uint4*>(&rows[(2 * p + 1) * RP + 8 * dc]) = r1[j];
+    }
+    store_cols<CP>(cols, tid);
+  }
+};
 
 // Store a wavefront's [32 tokens x D] result held transposed in MFMA accumulators (acc[md]
 // element 4 j + e is column 32 md + 8 j + 4 hi + e of token `row`), times `mul`.

@@ -38,7 +38,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq(const AttnBwdArgs b)
   constexpr int NT = 64 * NW, BM = 32 * NW;  // queries per block
   constexpr int BN = kAttnBN;
   constexpr int KP = D + 8;
-  constexpr int TP = BN + 8;
+  constexpr int TP = BN + kTPad;
   __shared__ __align__(16) T ks[BN * KP];  // K row-major (A operand of S^T)
   __shared__ __align__(16) T vs[BN * KP];  // V row-major (A operand of dP^T)
   __shared__ __align__(16) T kt_[D * TP];  // K^T (A operand of dQ^T)
@@ -86,12 +86,23 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq(const AttnBwdArgs b)
   const T* kbase = static_cast<const T*>(a.k) + (int64_t)kvh * D;
   const T* vbase = static_cast<const T*>(a.v) + (int64_t)kvh * D;
 
+  // K (row-major and transposed) and V (row-major) of the next key tile are read into
+  // registers while the current tile is computed
+  TilePairs<T, D, BN, NT> kp;
+  TileRows<T, D, BN, NT> vr;
+  if (start < kend) {
+    kp.load(kbase, a.k_rs, start, kend, tid);
+    vr.load(vbase, a.v_rs, start, kend, tid);
+  }
   for (int kt = start; kt < kend; kt += BN) {
     __syncthreads();
-    stage_rows<T, D, BN, KP, NT>(ks, kbase, a.k_rs, kt, kend, tid);
-    stage_rows<T, D, BN, KP, NT>(vs, vbase, a.v_rs, kt, kend, tid);
-    stage_cols<T, D, BN, TP, NT>(kt_, kbase, a.k_rs, kt, kend, tid);
+    kp.template store_both<KP, TP>(ks, kt_, tid);
+    vr.template store<KP>(vs, tid);
     __syncthreads();
+    if (kt + BN < kend) {
+      kp.load(kbase, a.k_rs, kt + BN, kend, tid);
+      vr.load(vbase, a.v_rs, kt + BN, kend, tid);
+    }
     if (!wave_live || kt > wq_last) continue;
 
     // one 32-key half at a time (fewer live registers: 3 wavefronts per SIMD instead of 2)
@@ -136,49 +147,6 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq(const AttnBwdArgs b)
                      a.scale);
 }
 
-// A [ROWS x D] tile prefetched into registers in row pairs: thread tid takes pairs
-// idx = tid + 256 j, rows (2p, 2p + 1) of 8-column chunk dc (p = idx % (ROWS / 2),
-// dc = idx / (ROWS / 2)); store() writes it to LDS row-major (pitch RP) and transposed (pitch
-// CP) in one go, so each global chunk is read once for both copies.
-template <typename T, int D, int ROWS, int NT = kAttnThreads>
-struct TilePairs {
-  static constexpr int N = (ROWS / 2) * (D / 8) / NT;
-  static_assert(N >= 1 && (ROWS / 2) * (D / 8) % NT == 0, "tile / block mismatch");
-  uint4 r0[N], r1[N];
-
-  __device__ __forceinline__ void load(const T* base, int64_t rs, int t0, int tend, int tid) {
-#pragma unroll
-    for (int j = 0; j < N; ++j) {
-      const int idx = tid + NT * j;
-      const int p = idx % (ROWS / 2), dc = idx / (ROWS / 2);
-      const int t = t0 + 2 * p;
-      r0[j] = t < tend ? *reinterpret_cast<const uint4*>(base + (int64_t)t * rs + 8 * dc)
-                       : make_uint4(0, 0, 0, 0);
-      r1[j] = t + 1 < tend ? *reinterpret_cast<const uint4*>(base + (int64_t)(t + 1) * rs + 8 * dc)
-                           : make_uint4(0, 0, 0, 0);
-    }
-  }
-
-  template <int RP, int CP>
-  __device__ __forceinline__ void store(T* rows, T* cols, int tid) const {
-#pragma unroll
-    for (int j = 0; j < N; ++j) {
-      const int idx = tid + NT * j;
-      const int p = idx % (ROWS / 2), dc = idx / (ROWS / 2);
-      *reinterpret_cast<uint4*>(&rows[(2 * p) * RP + 8 * dc]) = r0[j];
-      *reinterpret_cast<uint4*>(&rows[(2 * p + 1) * RP + 8 * dc]) = r1[j];
-      const uint32_t w0[4] = {r0[j].x, r0[j].y, r0[j].z, r0[j].w};
-      const uint32_t w1[4] = {r1[j].x, r1[j].y, r1[j].z, r1[j].w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t lo = (w0[e / 2] >> (16 * (e % 2))) & 0xffffu;
-        const uint32_t up = (w1[e / 2] >> (16 * (e % 2))) & 0xffffu;
-        *reinterpret_cast<uint32_t*>(&cols[(8 * dc + e) * CP + 2 * p]) = lo | (up << 16);
-      }
-    }
-  }
-};
-
 // Wavefronts per dK / dV block: 8 (256 keys) at D = 128, 4 (128 keys) at D = 64. With V's B
 // operands read from LDS the D = 128 kernel fits 2 wavefronts per SIMD (one 8-wave block per
 // CU, its LDS ~139 KiB); the staged Q / dO tiles are then shared by 8 wavefronts.
@@ -195,7 +163,7 @@ __global__ __launch_bounds__(64 * dkdv_waves<D>(), 2) void k_attn_bwd_dkdv(const
   const AttnArgs& a = b.f;
   constexpr int BQ = kAttnBQ;
   constexpr int RP = D + 8;   // row-major pitch
-  constexpr int CP = BQ + 8;  // transposed pitch
+  constexpr int CP = BQ + kTPad;  // transposed pitch
   __shared__ __align__(16) T qs[BQ * RP];   // Q row-major (A operand of S)
   __shared__ __align__(16) T ds_[BQ * RP];  // dO row-major (A operand of dP)
   __shared__ __align__(16) T qt_[D * CP];   // Q^T (A operand of dK^T)
@@ -229,8 +197,11 @@ __global__ __launch_bounds__(64 * dkdv_waves<D>(), 2) void k_attn_bwd_dkdv(const
 #pragma unroll
     for (int c = 0; c < D / 16; ++c) kb[c] = kok ? ld16<V8>(krow + 16 * c) : V8{};
   }
-  stage_rows<T, D, BK, RP, NT>(vsm, static_cast<const T*>(a.v) + (int64_t)kh * D, a.v_rs, k0, end,
-                               tid);
+  {
+    TileRows<T, D, BK, NT> vr;
+    vr.load(static_cast<const T*>(a.v) + (int64_t)kh * D, a.v_rs, k0, end, tid);
+    vr.template store<RP>(vsm, tid);
+  }
   const T* vlds = &vsm[(32 * w + lq) * RP + 8 * hi];
   f32x16 dka[D / 32], dva[D / 32];
 #pragma unroll
@@ -258,8 +229,8 @@ __global__ __launch_bounds__(64 * dkdv_waves<D>(), 2) void k_attn_bwd_dkdv(const
   for (int it = 0; it < items; ++it) {
     const int qt = k0 + (it % nqt) * BQ;
     __syncthreads();  // the previous item's LDS reads are done
-    pq.template store<RP, CP>(qs, qt_, tid);
-    pd.template store<RP, CP>(ds_, dt_, tid);
+    pq.template store_both<RP, CP>(qs, qt_, tid);
+    pd.template store_both<RP, CP>(ds_, dt_, tid);
     if (tid < BQ) {
       lse_s[tid] = lse_n;
       del_s[tid] = del_n;
