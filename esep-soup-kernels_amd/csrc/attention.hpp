@@ -16,7 +16,7 @@
 // operand), so each lane owns one query and 16 of a half's 32 scores; the other 16 sit in lane
 // l ^ 32, and a row max or sum is a register reduction plus one cross-half exchange. The probabilities go straight from the
 // score registers into O^T += V^T P^T: the contraction over keys is permuted so that the B
-// operand a lane needs is exactly the scores it holds, and V^T (staged transposed in LDS) is
+// operand a lane needs is exactly the scores it holds, and V^T (read transposed out of the row-major V tile) is
 // read in the same permuted key order.
 //
 // MFMA lane layouts (checked on the device against a CPU product): v_mfma_f32_32x32x16_{bf16,f16}
@@ -93,11 +93,12 @@ struct Mfma<_Float16> {
   }
 };
 
-// Padding (elements) of the transposed LDS tiles (V^T, K^T, Q^T, dO^T: 64 columns): a pitch of
-// 68 bf16 = 34 dwords puts the 32 rows an 8-byte operand read touches on 32 distinct bank pairs
-// (34 r mod 64 covers every even bank once); +8 (36 dwords) left 2-way conflicts and measured
-// 6% slower in the backward.
-constexpr int kTPad = 4;
+// Row pitch (elements) of the row-major LDS tiles: D + kRowPad. At D = 128 the pitch is 152 bf16
+// = 76 dwords, rows at bank offsets 12 r mod 64: the 8 rows a transposing operand read (ld_tr)
+// touches and the 16 rows of a 16-byte row read both spread over the banks. Measured on the
+// backward at config 5: +8 (68 dwords) 11.6 ms, +16 11.4, +24 10.8, +32 (16 r: 4-way row
+// conflicts) 13.2, +40 10.7, +48 11.0.
+constexpr int kRowPad = 24;
 
 // 2^x on the hardware's v_exp_f32 alone (no denormal-range scaling: results below 2^-126 flush
 // to 0, far below what a probability contributes next to the sums they enter).
@@ -108,12 +109,24 @@ __device__ __forceinline__ V ld16(const void* p) {
   return __builtin_bit_cast(V, *reinterpret_cast<const uint4*>(p));
 }
 
-// 8 elements from two 4-element (8-byte) halves.
-template <typename V>
-__device__ __forceinline__ V ld8x2(const void* lo, const void* hi) {
-  const uint2 a = *reinterpret_cast<const uint2*>(lo);
-  const uint2 b = *reinterpret_cast<const uint2*>(hi);
-  return __builtin_bit_cast(V, make_uint4(a.x, a.y, b.x, b.y));
+typedef short s16x4 __attribute__((ext_vector_type(4)));
+typedef short s16x8 __attribute__((ext_vector_type(8)));
+
+// A operand (8 elements) of v_mfma_f32_32x32x16 read transposed out of a row-major LDS matrix M
+// (pitch P elements): A[i][kk] = M[r0 + pi(kk)][c0 + i], i < 32, kk < 16, where pi is the
+// permuted contraction order of the score accumulators (kk 0-3, 4-7, 8-11, 12-15 -> rows 0-3,
+// 8-11, 4-7, 12-15: the rows a lane holds in its B operand). Two ds_read_b64_tr_b16: within a
+// 16-lane group the hardware hands lane j, slot k, element j % 4 of the 8-byte segment
+// addressed by lane 4 k + j / 4 (checked on the device), so lane 16 g + 4 k + m addresses row
+// r0 + 4 (g / 2) + k (+ 8 for the second read), columns c0 + 16 (g % 2) + 4 m .. + 3.
+template <typename V, int P, typename T>
+__device__ __forceinline__ V ld_tr(const T* M, int r0, int c0, int lane) {
+  const int g = lane >> 4, k = (lane >> 2) & 3, m = lane & 3;
+  T* p = const_cast<T*>(M) + (r0 + 4 * (g >> 1) + k) * P + c0 + 16 * (g & 1) + 4 * m;
+  typedef __attribute__((address_space(3))) s16x4* lds_ptr;
+  const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr)(p));
+  const s16x4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr)(p + 8 * P));
+  return __builtin_bit_cast(V, __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7));
 }
 
 // Sequence s's token range [start, end), clamped into [0, T].
@@ -154,60 +167,6 @@ struct TileRows {
       const int idx = tid + NT * j;
       *reinterpret_cast<uint4*>(&dst[(idx % ROWS) * P + 8 * (idx / ROWS)]) = r[j];
     }
-  }
-};
-
-// A [ROWS x D] tile in row pairs for a transposed copy: thread tid takes pairs idx = tid + NT j,
-// rows (2p, 2p + 1) of 8-column chunk dc (p = idx % (ROWS / 2), dc = idx / (ROWS / 2)).
-// store_cols() writes the tile transposed ([D x ROWS], pitch CP: one dword per column holding
-// the two rows' values); store_both() also writes it row-major (pitch RP), so each global chunk
-// is read once for both copies.
-template <typename T, int D, int ROWS, int NT = kAttnThreads>
-struct TilePairs {
-  static constexpr int N = (ROWS / 2) * (D / 8) / NT;
-  static_assert(N >= 1 && (ROWS / 2) * (D / 8) % NT == 0, "tile / block mismatch");
-  uint4 r0[N], r1[N];
-
-  __device__ __forceinline__ void load(const T* base, int64_t rs, int t0, int tend, int tid) {
-#pragma unroll
-    for (int j = 0; j < N; ++j) {
-      const int idx = tid + NT * j;
-      const int p = idx % (ROWS / 2), dc = idx / (ROWS / 2);
-      const int t = t0 + 2 * p;
-      r0[j] = t < tend ? *reinterpret_cast<const uint4*>(base + (int64_t)t * rs + 8 * dc)
-                       : make_uint4(0, 0, 0, 0);
-      r1[j] = t + 1 < tend ? *reinterpret_cast<const uint4*>(base + (int64_t)(t + 1) * rs + 8 * dc)
-                           : make_uint4(0, 0, 0, 0);
-    }
-  }
-
-  template <int CP>
-  __device__ __forceinline__ void store_cols(T* cols, int tid) const {
-#pragma unroll
-    for (int j = 0; j < N; ++j) {
-      const int idx = tid + NT * j;
-      const int p = idx % (ROWS / 2), dc = idx / (ROWS / 2);
-      const uint32_t w0[4] = {r0[j].x, r0[j].y, r0[j].z, r0[j].w};
-      const uint32_t w1[4] = {r1[j].x, r1[j].y, r1[j].z, r1[j].w};
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t lo = (w0[e / 2] >> (16 * (e % 2))) & 0xffffu;
-        const uint32_t up = (w1[e / 2] >> (16 * (e % 2))) & 0xffffu;
-        *reinterpret_cast<uint32_t*>(&cols[(8 * dc + e) * CP + 2 * p]) = lo | (up << 16);
-      }
-    }
-  }
-
-  template <int RP, int CP>
-  __device__ __forceinline__ void store_both(T* rows, T* cols, int tid) const {
-#pragma unroll
-    for (int j = 0; j < N; ++j) {
-      const int idx = tid + NT * j;
-      const int p = idx % (ROWS / 2), dc = idx / (ROWS / 2);
-      *reinterpret_cast<uint4*>(&rows[(2 * p) * RP + 8 * dc]) = r0[j];
-      *reinterpret_cast<uint4*>(&rows[(2 * p + 1) * RP + 8 * dc]) = r1[j];
-    }
-    store_cols<CP>(cols, tid);
   }
 };
 

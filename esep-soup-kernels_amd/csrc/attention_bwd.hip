@@ -7,8 +7,8 @@
 // k_attn_bwd_dq: one block per (128 queries, query head) as in the forward. It first computes
 // delta for its queries (stored to the delta workspace), then walks the causal key tiles:
 // S^T = K Q^T and dP^T = V dO^T with the wave's Q and dO held in registers as B operands, and
-// dQ^T += K^T dS^T with K^T staged transposed in LDS and dS^T fed from registers in the permuted
-// key order (the forward's P V trick).
+// dQ^T += K^T dS^T with K^T read transposed (ds_read_b64_tr_b16) out of the row-major K tile and
+// dS^T fed from registers in the permuted key order (the forward's P V trick).
 //
 // k_attn_bwd_dkdv: one block per (256 keys at D = 128, 128 at D = 64; kv head; part of the kv
 // head's query heads); wavefront w owns keys 32w..32w+31 and holds their K in registers as B
@@ -16,7 +16,7 @@
 // walks, for each of its query heads in turn and each query tile of 64 at or after its keys
 // (the next tile prefetched into registers during the current one), S = Q K^T and dP = dO V^T (Q and dO
 // staged row-major in LDS as A operands), then dV^T += dO^T P and dK^T += Q^T dS (Q^T and dO^T
-// staged transposed, P and dS from registers in the permuted query order). Each key's dK and
+// read transposed out of the same tiles, P and dS from registers in the permuted query order). Each key's dK and
 // dV are summed by one lane in a fixed order over heads and query tiles; with the heads split
 // over several blocks (short inputs, to fill the GPU), each part writes fp32 partials and
 // k_attn_dkdv_reduce adds them in part order, so the result is bitwise reproducible. Runs after
@@ -37,11 +37,9 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq(const AttnBwdArgs b)
   const AttnArgs& a = b.f;
   constexpr int NT = 64 * NW, BM = 32 * NW;  // queries per block
   constexpr int BN = kAttnBN;
-  constexpr int KP = D + 8;
-  constexpr int TP = BN + kTPad;
-  __shared__ __align__(16) T ks[BN * KP];  // K row-major (A operand of S^T)
+  constexpr int KP = D + kRowPad;
+  __shared__ __align__(16) T ks[BN * KP];  // K row-major (A operand of S^T; read transposed for dQ^T)
   __shared__ __align__(16) T vs[BN * KP];  // V row-major (A operand of dP^T)
-  __shared__ __align__(16) T kt_[D * TP];  // K^T (A operand of dQ^T)
 
   const int seq = blockIdx.z, h = blockIdx.y;
   int start, end;
@@ -86,21 +84,19 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq(const AttnBwdArgs b)
   const T* kbase = static_cast<const T*>(a.k) + (int64_t)kvh * D;
   const T* vbase = static_cast<const T*>(a.v) + (int64_t)kvh * D;
 
-  // K (row-major and transposed) and V (row-major) of the next key tile are read into
-  // registers while the current tile is computed
-  TilePairs<T, D, BN, NT> kp;
-  TileRows<T, D, BN, NT> vr;
+  // K and V of the next key tile are read into registers while the current tile is computed
+  TileRows<T, D, BN, NT> kr, vr;
   if (start < kend) {
-    kp.load(kbase, a.k_rs, start, kend, tid);
+    kr.load(kbase, a.k_rs, start, kend, tid);
     vr.load(vbase, a.v_rs, start, kend, tid);
   }
   for (int kt = start; kt < kend; kt += BN) {
     __syncthreads();
-    kp.template store_both<KP, TP>(ks, kt_, tid);
+    kr.template store<KP>(ks, tid);
     vr.template store<KP>(vs, tid);
     __syncthreads();
     if (kt + BN < kend) {
-      kp.load(kbase, a.k_rs, kt + BN, kend, tid);
+      kr.load(kbase, a.k_rs, kt + BN, kend, tid);
       vr.load(vbase, a.v_rs, kt + BN, kend, tid);
     }
     if (!wave_live || kt > wq_last) continue;
@@ -130,16 +126,13 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq(const AttnBwdArgs b)
         const float p = exp2_fast(fmaf(s[i], a.scale_log2, -lse2));
         dsb[i / 8][i % 8] = (T)(p * (dp[i] - delta));
       }
-      // dQ^T += K^T dS^T, keys in the permuted order of dsb
+      // dQ^T += K^T dS^T, keys in the permuted order of dsb, K^T read transposed out of ks
 #pragma unroll
-      for (int md = 0; md < D / 32; ++md) {
-        const T* trow = &kt_[(32 * md + lq) * TP + 4 * hi];
+      for (int md = 0; md < D / 32; ++md)
 #pragma unroll
-        for (int c2 = 0; c2 < 2; ++c2) {
-          const int kb = 32 * sb + 16 * c2;
-          dqa[md] = Mfma<T>::run(ld8x2<V8>(trow + kb, trow + kb + 8), dsb[c2], dqa[md]);
-        }
-      }
+        for (int c2 = 0; c2 < 2; ++c2)
+          dqa[md] = Mfma<T>::run(ld_tr<V8, KP>(ks, 32 * sb + 16 * c2, 32 * md, lane), dsb[c2],
+                                 dqa[md]);
     }
   }
   if (!qok) return;
@@ -162,12 +155,9 @@ __global__ __launch_bounds__(64 * dkdv_waves<D>(), 2) void k_attn_bwd_dkdv(const
   using V8 = typename Mfma<T>::v8;
   const AttnArgs& a = b.f;
   constexpr int BQ = kAttnBQ;
-  constexpr int RP = D + 8;   // row-major pitch
-  constexpr int CP = BQ + kTPad;  // transposed pitch
-  __shared__ __align__(16) T qs[BQ * RP];   // Q row-major (A operand of S)
-  __shared__ __align__(16) T ds_[BQ * RP];  // dO row-major (A operand of dP)
-  __shared__ __align__(16) T qt_[D * CP];   // Q^T (A operand of dK^T)
-  __shared__ __align__(16) T dt_[D * CP];   // dO^T (A operand of dV^T)
+  constexpr int RP = D + kRowPad;  // row-major pitch
+  __shared__ __align__(16) T qs[BQ * RP];   // Q row-major (A operand of S; transposed, of dK^T)
+  __shared__ __align__(16) T ds_[BQ * RP];  // dO row-major (A operand of dP; transposed, of dV^T)
   __shared__ __align__(16) float lse_s[BQ];
   __shared__ __align__(16) float del_s[BQ];
   __shared__ __align__(16) T vsm[BK * RP];  // this block's V rows (B operands of dP)
@@ -211,7 +201,7 @@ __global__ __launch_bounds__(64 * dkdv_waves<D>(), 2) void k_attn_bwd_dkdv(const
   // into registers while the current one is computed.
   const int nqt = (end - k0 + BQ - 1) / BQ;
   const int items = gs * nqt;
-  TilePairs<T, D, BQ, NT> pq, pd;
+  TileRows<T, D, BQ, NT> pq, pd;
   float lse_n = 0.f, del_n = 0.f;
   auto prefetch = [&](int it) {
     const int h = h0 + it / nqt, qt = k0 + (it % nqt) * BQ;
@@ -229,8 +219,8 @@ __global__ __launch_bounds__(64 * dkdv_waves<D>(), 2) void k_attn_bwd_dkdv(const
   for (int it = 0; it < items; ++it) {
     const int qt = k0 + (it % nqt) * BQ;
     __syncthreads();  // the previous item's LDS reads are done
-    pq.template store_both<RP, CP>(qs, qt_, tid);
-    pd.template store_both<RP, CP>(ds_, dt_, tid);
+    pq.template store<RP>(qs, tid);
+    pd.template store<RP>(ds_, tid);
     if (tid < BQ) {
       lse_s[tid] = lse_n;
       del_s[tid] = del_n;
@@ -278,16 +268,13 @@ __global__ __launch_bounds__(64 * dkdv_waves<D>(), 2) void k_attn_bwd_dkdv(const
       }
       // dV^T += dO^T P and dK^T += Q^T dS, queries in the permuted order of pb / sb_
 #pragma unroll
-      for (int md = 0; md < D / 32; ++md) {
-        const T* dtr = &dt_[(32 * md + lq) * CP + 4 * hi];
-        const T* qtr = &qt_[(32 * md + lq) * CP + 4 * hi];
+      for (int md = 0; md < D / 32; ++md)
 #pragma unroll
         for (int c2 = 0; c2 < 2; ++c2) {
           const int rb = 32 * qh + 16 * c2;
-          dva[md] = Mfma<T>::run(ld8x2<V8>(dtr + rb, dtr + rb + 8), pb[c2], dva[md]);
-          dka[md] = Mfma<T>::run(ld8x2<V8>(qtr + rb, qtr + rb + 8), sb_[c2], dka[md]);
+          dva[md] = Mfma<T>::run(ld_tr<V8, RP>(ds_, rb, 32 * md, lane), pb[c2], dva[md]);
+          dka[md] = Mfma<T>::run(ld_tr<V8, RP>(qs, rb, 32 * md, lane), sb_[c2], dka[md]);
         }
-      }
     }
   }
   if (!kok) return;

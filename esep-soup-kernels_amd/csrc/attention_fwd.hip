@@ -12,10 +12,9 @@ template <typename T, int D>
 __global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd(const AttnArgs a) {
   using V8 = typename Mfma<T>::v8;
   constexpr int BN = kAttnBN;
-  constexpr int KP = D + 8;   // K row pitch in LDS (elements): rows land on different banks
-  constexpr int VP = BN + kTPad;  // V^T row pitch in LDS (elements)
+  constexpr int KP = D + kRowPad;  // row pitch of the K and V tiles in LDS (elements)
   __shared__ __align__(16) T ks[BN * KP];
-  __shared__ __align__(16) T vt[D * VP];
+  __shared__ __align__(16) T vs[BN * KP];
 
   const int seq = blockIdx.z, h = blockIdx.y;
   int start, end;  // clamped into [0, T]: malformed offsets stay in bounds
@@ -49,17 +48,16 @@ __global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd(const AttnArgs a) 
   const T* vbase = static_cast<const T*>(a.v) + (int64_t)kvh * D;
 
   for (int kt = start; kt < kend; kt += BN) {
-    // K (row-major) and V (transposed) of the tile: every global read is issued before the
-    // barrier, one memory round trip per tile; keys past kend read 0. (Reading the next tile
-    // during the current one needs 32 more registers: 2 wavefronts per SIMD instead of 3,
-    // measured 15% slower.)
-    TileRows<T, D, BN> kr;
-    TilePairs<T, D, BN> vp;
+    // K and V of the tile, row-major: every global read is issued before the barrier, one
+    // memory round trip per tile; keys past kend read 0. (Reading the next tile during the
+    // current one needs 32 more registers: 2 wavefronts per SIMD instead of 3, measured 15%
+    // slower.)
+    TileRows<T, D, BN> kr, vr;
     kr.load(kbase, a.k_rs, kt, kend, tid);
-    vp.load(vbase, a.v_rs, kt, kend, tid);
+    vr.load(vbase, a.v_rs, kt, kend, tid);
     __syncthreads();  // the previous tile's LDS reads are done
     kr.template store<KP>(ks, tid);
-    vp.template store_cols<VP>(vt, tid);
+    vr.template store<KP>(vs, tid);
     __syncthreads();
     if (!wave_live || kt > wq_last) continue;  // every key of the tile is after this wave's queries
 
@@ -109,17 +107,15 @@ __global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd(const AttnArgs a) 
 #pragma unroll
         for (int md = 0; md < D / 32; ++md) oacc[md] *= alpha;
       }
-      // O^T += V^T P^T over the 32 keys, contraction in the permuted key order of pb: element e
-      // of chunk c2 is key 32 sb + 16 c2 + 8 (e / 4) + 4 hi + e % 4.
+      // O^T += V^T P^T over the 32 keys, contraction in the permuted key order of pb (element
+      // e of chunk c2 is key 32 sb + 16 c2 + 8 (e / 4) + 4 hi + e % 4); V^T read transposed out
+      // of the row-major V tile.
 #pragma unroll
-      for (int md = 0; md < D / 32; ++md) {
-        const T* vrow = &vt[(32 * md + lq) * VP + 4 * hi];
+      for (int md = 0; md < D / 32; ++md)
 #pragma unroll
-        for (int c2 = 0; c2 < 2; ++c2) {
-          const int kb = 32 * sb + 16 * c2;
-          oacc[md] = Mfma<T>::run(ld8x2<V8>(vrow + kb, vrow + kb + 8), pb[c2], oacc[md]);
-        }
-      }
+        for (int c2 = 0; c2 < 2; ++c2)
+          oacc[md] = Mfma<T>::run(ld_tr<V8, KP>(vs, 32 * sb + 16 * c2, 32 * md, lane), pb[c2],
+                                  oacc[md]);
     }
   }
 
