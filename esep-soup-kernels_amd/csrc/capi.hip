@@ -576,6 +576,44 @@ int esep_nf4_dequant(const void* packed, const uint8_t* absmax, const float* abs
   return e == hipSuccess ? 0 : hip_fail(e, "nf4_dequant launch");
 }
 
+static_assert(ESEP_NF4_MULTI_MAX == esep::kNf4MultiMax, "multi-weight limit of the ABI and the kernel");
+
+int esep_nf4_dequant_multi(const esep_nf4_weight* weights, int n_weights, int out_dt,
+                           void* stream) {
+  g_err[0] = 0;
+  if (!float_dt(out_dt))
+    return fail(ESEP_EINVAL, "nf4_dequant_multi: bad output dtype code %d", out_dt);
+  if (weights == nullptr || n_weights < 1 || n_weights > ESEP_NF4_MULTI_MAX)
+    return fail(ESEP_EINVAL, "nf4_dequant_multi: need 1..%d weights (got %d)", ESEP_NF4_MULTI_MAX,
+                n_weights);
+  esep::Nf4Multi m{};
+  m.n = n_weights;
+  m.q0[0] = 0;
+  for (int i = 0; i < n_weights; ++i) {
+    const esep_nf4_weight& w = weights[i];
+    if (w.n_blocks < 0 || w.n_blocks > (int64_t{1} << 40))
+      return fail(ESEP_ESHAPE, "nf4_dequant_multi: weight %d n_blocks=%lld out of range", i,
+                  (long long)w.n_blocks);
+    if (w.packed == nullptr || w.absmax == nullptr || w.absmax2 == nullptr ||
+        w.code2 == nullptr || w.offset == nullptr || w.nf4 == nullptr || w.out == nullptr)
+      return fail(ESEP_EINVAL, "nf4_dequant_multi: weight %d: every pointer is required", i);
+    if ((reinterpret_cast<uintptr_t>(w.packed) & 7) || !aligned16(w.out))
+      return fail(ESEP_EALIGN,
+                  "nf4_dequant_multi: weight %d: packed needs 8-byte and out 16-byte alignment", i);
+    m.w[i] = esep::Nf4Args{w.packed, w.absmax, w.absmax2, w.code2, w.offset, w.nf4, w.out,
+                           w.n_blocks};
+    m.q0[i + 1] = m.q0[i] + 4 * w.n_blocks;
+  }
+  for (int i = n_weights; i < esep::kNf4MultiMax; ++i) m.q0[i + 1] = m.q0[n_weights];
+  if (m.q0[n_weights] / 256 >= 0x7fffffffLL)
+    return fail(ESEP_ESHAPE, "nf4_dequant_multi: too many blocks for one launch");
+  bool sup = false;
+  const hipError_t e =
+      esep::launch_nf4_dequant_multi(m, out_dt, static_cast<hipStream_t>(stream), &sup);
+  if (!sup) return fail(ESEP_EINVAL, "nf4_dequant_multi: unsupported output dtype");
+  return e == hipSuccess ? 0 : hip_fail(e, "nf4_dequant_multi launch");
+}
+
 int esep_head_row_softmax(void* z, int64_t ld, const int64_t* target, const float* cew,
                           float* lse, float* tlogit, float* ent, int32_t* amax, int64_t rows,
                           int64_t V, int write_g, float g_scale, int dt, void* stream) {

@@ -20,4 +20,16 @@ struct Nf4Args {
 
 hipError_t launch_nf4_dequant(const Nf4Args& a, int out_dt, hipStream_t s, bool* supported);
 
+constexpr int kNf4MultiMax = 8;
+
+// Up to kNf4MultiMax weights decoded by one launch; weight i covers the global 8-packed-byte
+// units [q0[i], q0[i + 1]) (4 per 64-element scale block).
+struct Nf4Multi {
+  Nf4Args w[kNf4MultiMax];
+  int64_t q0[kNf4MultiMax + 1];
+  int n;
+};
+
+hipError_t launch_nf4_dequant_multi(const Nf4Multi& m, int out_dt, hipStream_t s, bool* supported);
+
 }  // namespace esep

@@ -50,6 +50,7 @@ SIGNATURES = {
     "esep_nf4_dequant": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _vp]),
     "esep_head_row_softmax": (_i32, [_vp, _i64, _vp, _vp, _vp, _vp, _vp, _vp, _i64, _i64, _i32,
                                      _f32, _i32, _vp]),
+    "esep_nf4_dequant_multi": (_i32, [_vp, _i32, _i32, _vp]),
     "esep_lora_dropout_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _f32, _i32, _i32, _vp]),
     "esep_swiglu_bwd": (_i32, [_vp, _vp, _vp, _vp, _vp, _i64, _i32, _vp]),
     "esep_attn_bwd": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp,
@@ -447,6 +448,49 @@ def nf4_dequant(packed, absmax, absmax2, code2, offset, nf4, out, name="_nf4_deq
     rc = lib().esep_nf4_dequant(_p(packed), _p(absmax.contiguous()), _p(absmax2), _p(code2),
                                 _p(offset), _p(nf4), _p(out), dtype_code(out.dtype), nb, _stream(dev))
     _check(rc, "esep_nf4_dequant")
+    _record(name)
+
+
+class Nf4Weight(ctypes.Structure):
+    """esep_nf4_weight (include/esep_body.h)."""
+    _fields_ = [("packed", _vp), ("absmax", _vp), ("absmax2", _vp), ("code2", _vp),
+                ("offset", _vp), ("nf4", _vp), ("out", _vp), ("n_blocks", _i64)]
+
+
+NF4_MULTI_MAX = 8
+
+
+def nf4_dequant_multi(items, name="_nf4_dequant_multi"):
+    """Several NF4 weights in one launch (esep_nf4_dequant_multi). items: sequence of
+    (packed, absmax, absmax2, code2, offset, nf4, out) tuples, each as for nf4_dequant; every out
+    shares one dtype."""
+    if not 1 <= len(items) <= NF4_MULTI_MAX:
+        raise EsepError(f"1..{NF4_MULTI_MAX} weights per launch")
+    dev = _dev(*[t for it in items for t in it])
+    arr = (Nf4Weight * len(items))()
+    dts = set()
+    for k, (packed, absmax, absmax2, code2, offset, nf4, out) in enumerate(items):
+        nb = absmax.numel()
+        if packed.dtype != torch.uint8 or packed.numel() != nb * 32 or absmax.dtype != torch.uint8:
+            raise EsepError("packed must hold n_blocks * 32 uint8 and absmax n_blocks uint8")
+        for t, nm in ((absmax2, "absmax2"), (code2, "code2"), (offset, "offset"), (nf4, "nf4")):
+            if t.dtype != torch.float32 or not t.is_contiguous():
+                raise EsepError(f"{nm} must be a contiguous fp32 tensor")
+        if (absmax2.numel() < (nb + 255) // 256 or code2.numel() < 256 or nf4.numel() < 16
+                or offset.numel() < 1):
+            raise EsepError("nf4 tables too small")
+        if out.numel() != nb * 64 or not out.is_contiguous():
+            raise EsepError("out must be n_blocks * 64 contiguous elements")
+        if not (packed.is_contiguous() and absmax.is_contiguous()):
+            raise EsepError("packed and absmax must be contiguous")
+        dts.add(out.dtype)
+        arr[k] = Nf4Weight(_p(packed), _p(absmax), _p(absmax2), _p(code2), _p(offset), _p(nf4),
+                           _p(out), nb)
+    if len(dts) != 1:
+        raise EsepError("every output must share one dtype")
+    rc = lib().esep_nf4_dequant_multi(ctypes.cast(arr, _vp), len(items), dtype_code(dts.pop()),
+                                      _stream(dev))
+    _check(rc, "esep_nf4_dequant_multi")
     _record(name)
 
 

@@ -54,17 +54,25 @@ def dequantize_nf4(packed, quant_state, out=None, dtype=torch.float16):
 
 def dequantize_nf4_multi(weights, quant_states, out=None, dtype=torch.float16):
     """W_cat = cat([dequantize_nf4(w, qs) ...], 0) written straight into one [sum N_i, K] buffer
-    (one launch per weight, no copy); each slice bit-identical to dequantize_nf4."""
+    by one launch (esep_nf4_dequant_multi, up to 8 weights per launch; the reference's
+    multi-weight kernel takes 3, dequant.py:116-205); each slice bit-identical to
+    dequantize_nf4."""
     K = quant_states[0].shape[1]
     if any(qs.shape[1] != K for qs in quant_states):
         raise ValueError("weights must share K")
     n_total = sum(qs.shape[0] for qs in quant_states)
     if out is None:
         out = torch.empty((n_total, K), dtype=dtype, device=weights[0].device)
-    r = 0
+    items, r = [], 0
     for w, qs in zip(weights, quant_states):
-        dequantize_nf4(w, qs, out=out[r:r + qs.shape[0]])
+        qs2 = qs.state2
+        items.append((w.reshape(-1) if w.is_contiguous() else w.contiguous().reshape(-1),
+                      qs.absmax.contiguous(), qs2.absmax.to(torch.float32).contiguous(),
+                      qs2.code.to(torch.float32).contiguous(), _offset(qs),
+                      qs.code.to(torch.float32).contiguous(), out[r:r + qs.shape[0]].reshape(-1)))
         r += qs.shape[0]
+    for i in range(0, len(items), _hip.NF4_MULTI_MAX):
+        _hip.nf4_dequant_multi(items[i:i + _hip.NF4_MULTI_MAX])
     return out
 
 

@@ -264,6 +264,26 @@ int esep_nf4_dequant(const void* packed, const uint8_t* absmax, const float* abs
                      int out_dt, int64_t n_blocks, void* stream);
 
 /*
+ * Several NF4 weights in one launch. Replaces the reference's one-launch multi-weight kernel
+ * (solution/nf4/dequant.py:129-166 nf4_dequant_multi_kernel, launched by dequantize_nf4_multi
+ * :185-205, up to 3 weights into one W_cat): each weight decodes exactly as esep_nf4_dequant (bit
+ * for bit) into its own `out` (slices of one W_cat, or separate buffers). `weights` is a host
+ * array of 1 .. ESEP_NF4_MULTI_MAX entries, read during the call (copied into the launch).
+ */
+#define ESEP_NF4_MULTI_MAX 8
+typedef struct {
+  const void* packed;     /* n_blocks * 32 bytes, 8-byte aligned */
+  const uint8_t* absmax;  /* [n_blocks] */
+  const float* absmax2;   /* [ceil(n_blocks / 256)] */
+  const float* code2;     /* [256] */
+  const float* offset;    /* one fp32 in device memory */
+  const float* nf4;       /* [16] */
+  void* out;              /* n_blocks * 64 elements of out_dt, 16-byte aligned */
+  int64_t n_blocks;
+} esep_nf4_weight;
+int esep_nf4_dequant_multi(const esep_nf4_weight* weights, int n_weights, int out_dt, void* stream);
+
+/*
  * Fused LM head: softmax statistics and dlogits of one logits chunk. Replaces the reference's
  * Triton launch at solution/head/op.py:79-84 (_run; kernel head_row_softmax_kernel,
  * solution/head/kernels.py:37-93). For each row r of z ([rows, V] of dt, row stride ld):

@@ -187,3 +187,25 @@ def test_head_row_softmax_validation():
     assert call(cew=None) == -1  # the CE weights decide which rows get g
     assert call(z=17) == -3
     assert call(rows=0) == 0  # nothing to do, nothing launched
+
+
+def test_nf4_dequant_multi_validation():
+    """esep_nf4_dequant_multi checks the weight count, every weight's pointers, sizes and
+    alignment, and the output dtype before launching anything."""
+    lib = _hip.lib()
+
+    def call(n=2, dt=1, **kw):
+        arr = (_hip.Nf4Weight * 9)()
+        for i in range(9):
+            f = dict(packed=64, absmax=64, absmax2=64, code2=64, offset=64, nf4=64, out=64, n_blocks=4)
+            if i == 1:
+                f.update(kw)
+            arr[i] = _hip.Nf4Weight(*f.values())
+        return lib.esep_nf4_dequant_multi(ctypes.cast(arr, ctypes.c_void_p), n, dt, None)
+
+    assert call(n=0) == -1 and call(n=9) == -1
+    assert lib.esep_nf4_dequant_multi(None, 1, 1, None) == -1
+    assert call(dt=3) == -1
+    assert call(out=None) == -1 and b"weight 1" in lib.esep_last_error()
+    assert call(n_blocks=-1) == -2
+    assert call(packed=68) == -3 and call(out=72) == -3

@@ -7,7 +7,9 @@ indices, random second-level scales, code tables and offset, at the four weight 
 Qwen2.5-1.5B (reference test_nf4.py:16) and ragged block counts; fp16 out (the reference's) plus
 bf16 and fp32. A weight quantized by the oracle's QLoRA-style quantizer goes through
 dequantize_nf4 with a bitsandbytes-shaped quant state, the multi-weight form writes bit-identical
-slices, and NF4Linear matches a dense linear on the dequantized weight in both directions.
+slices, and NF4Linear matches a dense linear on the dequantized weight in both directions. The
+one-launch multi-weight entry (esep_nf4_dequant_multi) decodes 8 weights of ragged sizes, each
+with its own tables, bit-identically to the oracle and to one single-weight launch per weight.
 """
 
 import types
@@ -92,3 +94,53 @@ def test_dequantize_nf4_api_multi_and_linear():
     assert torch.equal(y, yr) and torch.equal(dx, dxr)
     bad = types.SimpleNamespace(**{**vars(qs), "quant_type": "fp4"})
     assert not nf4.supported(bad)
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16, torch.float32],
+                         ids=["fp16", "bf16", "fp32"])
+def test_multi_launch_bit_exact(dtype):
+    """esep_nf4_dequant_multi: 8 weights of ragged block counts (some not a multiple of the
+    256-thread block, so blocks straddle weights) in one launch, each with its own tables, equal
+    bit for bit to the oracle and to one esep_nf4_dequant per weight; a single weight too."""
+    from solution.body import _hip
+
+    sizes = [1, 3, 255, 256, 257, 1000, 6144, 4097]
+    items, wants, singles = [], [], []
+    for k, nb in enumerate(sizes):
+        packed, absmax, absmax2, code2, offset = _random_state(nb, seed=100 + k)
+        nf4 = np.sort(np.random.default_rng(k).standard_normal(16)).astype(np.float32)
+        t = (_dev(packed), _dev(absmax), _dev(absmax2), _dev(code2),
+             _dev(np.array([offset], dtype=np.float32)), _dev(nf4))
+        out = torch.full((nb * 64,), float("nan"), device=DEV, dtype=dtype)
+        items.append(t + (out,))
+        want32 = ref.dequantize_nf4(packed, absmax, absmax2, code2, offset, nf4=nf4,
+                                    out_dtype=np.float32)
+        wants.append(torch.from_numpy(want32).to(dtype))
+        single = torch.empty_like(out)
+        _hip.nf4_dequant(*t, single)
+        singles.append(single)
+    with _hip.count_launches() as names:
+        _hip.nf4_dequant_multi(items)
+    assert names == ["_nf4_dequant_multi"]
+    for it, want, single in zip(items, wants, singles):
+        assert torch.equal(it[-1].cpu(), want)
+        assert torch.equal(it[-1], single)
+    one = torch.empty_like(items[5][-1])
+    _hip.nf4_dequant_multi([items[5][:-1] + (one,)])
+    assert torch.equal(one, singles[5])
+
+
+def test_dequantize_nf4_multi_one_launch_per_eight():
+    from solution import nf4
+    from solution.body import _hip
+
+    rng = np.random.default_rng(2)
+    ws = [(rng.standard_normal((n, 128)) * 0.02).astype(np.float32) for n in (96, 32, 64) * 3]
+    states = [_quant_state(w) for w in ws]
+    with _hip.count_launches() as names:
+        cat = nf4.dequantize_nf4_multi([s[0] for s in states], [s[1] for s in states])
+    assert names == ["_nf4_dequant_multi"] * 2  # 9 weights: 8 + 1
+    r = 0
+    for packed, qs, _ in states:
+        assert torch.equal(cat[r:r + qs.shape[0]], nf4.dequantize_nf4(packed, qs))
+        r += qs.shape[0]
