@@ -22,6 +22,7 @@
 // k_attn_dkdv_reduce adds them in part order, so the result is bitwise reproducible. Runs after
 // k_attn_bwd_dq (it reads delta).
 #include <cmath>
+#include <type_traits>
 
 #include "attention.hpp"
 
@@ -140,21 +141,17 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq(const AttnBwdArgs b)
                      a.scale);
 }
 
-// Wavefronts per dK / dV block: 8 (256 keys) at D = 128, 4 (128 keys) at D = 64. With V's B
-// operands read from LDS the D = 128 kernel fits 2 wavefronts per SIMD (one 8-wave block per
-// CU, its LDS ~139 KiB); the staged Q / dO tiles are then shared by 8 wavefronts.
-template <int D>
-constexpr int dkdv_waves() {
-  return D == 128 ? 8 : 4;
-}
-
-template <typename T, int D>
-__global__ __launch_bounds__(64 * dkdv_waves<D>(), 2) void k_attn_bwd_dkdv(const AttnBwdArgs b) {
-  constexpr int NW = dkdv_waves<D>();
+// dK / dV blocks: NW wavefronts (32 keys each) and query tiles of BQ rows. D = 128 takes two
+// shapes: 8 wavefronts (256 keys, one block per CU by LDS) when the query heads of a kv head
+// are split over blocks (short inputs: the split parts supply the parallelism), and 4 wavefronts
+// with 32-query tiles (two blocks per CU, each hiding the other's barriers) when they are not:
+// at config 5 the backward takes 8.4 ms with 4 and 10.8 ms with 8, at config 4 0.30 vs 0.28 ms.
+// D = 64 takes 4 wavefronts and 64-query tiles.
+template <typename T, int D, int NW, int BQ>
+__global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs b) {
   constexpr int NT = 64 * NW, BK = 32 * NW;
   using V8 = typename Mfma<T>::v8;
   const AttnArgs& a = b.f;
-  constexpr int BQ = kAttnBQ;
   constexpr int RP = D + kRowPad;  // row-major pitch
   __shared__ __align__(16) T qs[BQ * RP];   // Q row-major (A operand of S; transposed, of dK^T)
   __shared__ __align__(16) T ds_[BQ * RP];  // dO row-major (A operand of dP; transposed, of dV^T)
@@ -232,7 +229,7 @@ __global__ __launch_bounds__(64 * dkdv_waves<D>(), 2) void k_attn_bwd_dkdv(const
 
     // one 32-query half at a time
 #pragma unroll
-    for (int qh = 0; qh < 2; ++qh) {
+    for (int qh = 0; qh < BQ / 32; ++qh) {
       f32x16 s = f32x16{}, dp = f32x16{};
       const T* qrow = &qs[(32 * qh + lq) * RP + 8 * hi];
       const T* drow = &ds_[(32 * qh + lq) * RP + 8 * hi];
@@ -334,9 +331,19 @@ hipError_t bwd_run(const AttnBwdArgs& b, int max_seqlen, hipStream_t s) {
   hipLaunchKernelGGL((k_attn_bwd_dq<T, D, QW>), gq, dim3(64 * QW), 0, s, b);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
-  constexpr int NW = dkdv_waves<D>();
-  const dim3 gk((max_seqlen + 32 * NW - 1) / (32 * NW), b.f.HK * b.split, b.f.n_seq);
-  hipLaunchKernelGGL((k_attn_bwd_dkdv<T, D>), gk, dim3(64 * NW), 0, s, b);
+  auto dkdv = [&](auto nw, auto bq) {
+    constexpr int NW = decltype(nw)::value, BQ = decltype(bq)::value;
+    const dim3 gk((max_seqlen + 32 * NW - 1) / (32 * NW), b.f.HK * b.split, b.f.n_seq);
+    hipLaunchKernelGGL((k_attn_bwd_dkdv<T, D, NW, BQ>), gk, dim3(64 * NW), 0, s, b);
+  };
+  if constexpr (D == 128) {
+    if (b.split > 1)
+      dkdv(std::integral_constant<int, 8>{}, std::integral_constant<int, 64>{});
+    else
+      dkdv(std::integral_constant<int, 4>{}, std::integral_constant<int, 32>{});
+  } else {
+    dkdv(std::integral_constant<int, 4>{}, std::integral_constant<int, 64>{});
+  }
   e = hipGetLastError();
   if (e != hipSuccess || b.split == 1) return e;
   const int64_t quads = b.f.T * b.f.HK * D / 4;

@@ -144,3 +144,44 @@ def test_attn_bwd_deterministic():
         _hip.attn_bwd(q, k, v, o, do, lse, *g, cu, 300, 128 ** -0.5)
         runs.append(g)
     assert all(torch.equal(a, b) for a, b in zip(*runs))
+
+
+def test_attn_bwd_long_sequences_sampled_keys():
+    """A config-5-like shape (4 sequences of 4096, 28 / 4 heads, D = 128: enough key blocks that
+    the kernel does not split the query heads, so the 4-wavefront dK / dV kernel runs) checked on
+    sampled keys against float64 sums restated from the formulas (dV_j = sum_q P_qj dO_q,
+    dK_j = scale sum_q P_qj (dP_qj - delta_q) Q_q over the causal queries of every query head of
+    the kv head), with the kernel's own lse and O for P and delta."""
+    from solution.body import _hip
+
+    lengths, HQ, HK, D = [4096] * 4, 28, 4, 128
+    q, k, v, cu = _inputs(lengths, HQ, HK, D, torch.bfloat16, seed=31)
+    T = q.shape[0]
+    assert ((T + 255) // 256) * HK >= 256  # no split: the 4-wavefront kernel
+    do = torch.randn(q.shape, generator=gen(32)).to(torch.bfloat16).to(DEV)
+    scale = D ** -0.5
+    o = torch.empty_like(q)
+    lse = torch.empty((HQ, T), device=DEV)
+    _hip.attn_fwd(q, k, v, o, cu, 4096, scale, lse=lse)
+    dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
+    _hip.attn_bwd(q, k, v, o, do, lse, dq, dk, dv, cu, 4096, scale)
+    Q, K, V, DO, O, L = (np64(t) for t in (q, k, v, do, o, lse))
+    DK, DV = np64(dk), np64(dv)
+    G = HQ // HK
+    rng = np.random.default_rng(33)
+    for j in sorted(rng.choice(T, 24, replace=False)):
+        s0 = (j // 4096) * 4096
+        t = np.arange(j, s0 + 4096)  # causal queries of key j
+        for hk in range(HK):
+            gdk = np.zeros(D)
+            gdv = np.zeros(D)
+            for h in range(hk * G, (hk + 1) * G):
+                p = np.exp(scale * (Q[t, h] @ K[j, hk]) - L[h, t])
+                dp = DO[t, h] @ V[j, hk]
+                delta = np.sum(DO[t, h] * O[t, h], axis=1)
+                gdv += p @ DO[t, h]
+                gdk += scale * ((p * (dp - delta)) @ Q[t, h])
+            for name, got, want in (("dk", DK[j, hk], gdk), ("dv", DV[j, hk], gdv)):
+                err = np.abs(got - want)
+                assert np.all(err <= 1e-2 * np.abs(want).max() + 1e-2 * np.abs(want) + 1e-5), \
+                    (name, j, hk, err.max(), np.abs(want).max())
