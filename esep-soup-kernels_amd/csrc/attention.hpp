@@ -104,6 +104,18 @@ constexpr int kRowPad = 24;
 // to 0, far below what a probability contributes next to the sums they enter).
 __device__ __forceinline__ float exp2_fast(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// max / sum of a lane's value and lane l ^ 32's, equal in both lanes (v_permlane32_swap hands
+// each lane the pair {own, partner} without going through LDS; + and max are commutative, so
+// both halves get the same bits).
+__device__ __forceinline__ float pair_max(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return fmaxf(__int_as_float(r[0]), __int_as_float(r[1]));
+}
+__device__ __forceinline__ float pair_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_int(v), __float_as_int(v), false, false);
+  return __int_as_float(r[0]) + __int_as_float(r[1]);
+}
+
 template <typename V>
 __device__ __forceinline__ V ld16(const void* p) {
   return __builtin_bit_cast(V, *reinterpret_cast<const uint4*>(p));

@@ -73,7 +73,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq(const AttnBwdArgs b)
 #pragma unroll
       for (int e = 0; e < 8; ++e) delta = fmaf((float)db[c][e], (float)o8[e], delta);
     }
-    delta += __shfl_xor(delta, 32);
+    delta = pair_sum(delta);
     if (qok && hi == 0) b.delta[(int64_t)h * a.T + qi] = delta;
   }
   const float lse2 = qok ? a.lse[(int64_t)h * a.T + qi] * kLog2e : 0.f;

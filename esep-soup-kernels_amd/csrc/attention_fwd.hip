@@ -82,7 +82,7 @@ __global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd(const AttnArgs a) 
       float mx = acc[0];
 #pragma unroll
       for (int i = 1; i < 16; ++i) mx = fmaxf(mx, acc[i]);
-      mx = fmaxf(mx, __shfl_xor(mx, 32)) * a.scale_log2;
+      mx = pair_max(mx) * a.scale_log2;
       // Online softmax (base 2) with a lazy reference: the lane's m moves only when the half's
       // maximum exceeds it by more than 8, so p <= 2^8 (exact in bf16 / fp16 relative terms)
       // and O, l are rescaled only in the rare half-tiles where some lane's m moved.
@@ -101,7 +101,7 @@ __global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd(const AttnArgs a) 
         ps += p;
         pb[i / 8][i % 8] = (T)p;
       }
-      ps += __shfl_xor(ps, 32);
+      ps = pair_sum(ps);
       l = fmaf(l, alpha, ps);
       if (__any(grow)) {
 #pragma unroll
