@@ -46,8 +46,15 @@ void norm_shape(int64_t n, int* wpr, int* nv) {
   *nv = v < 2 ? 2 : v;
 }
 
-// Groups (rows in flight) per backward block of kBwdThreads threads.
-int bwd_groups(int wpr) { return esep::kBwdThreads / (64 * wpr); }
+// Row groups per backward block with a weight gradient: blocks of up to 512 threads (one row
+// group of wpr wavefronts when a row needs more). Measured on MI355X against 1024-thread blocks
+// (config 4 / config 5 backward per launch): 512 threads 19.2 / 247 us (with the P below),
+// 1024 threads 19.7 / 255 us, 768 19.6 / 265, 256 22.3 / 422.
+constexpr int kBwdBlockThreads = 512;
+int bwd_groups(int wpr) {
+  const int g = kBwdBlockThreads / (64 * wpr);
+  return g > 0 ? g : 1;
+}
 
 // LDS bytes of the backward's weight-gradient tree for gpb groups with NV chunks per lane:
 // the most slots any tree level parks at once, each NV * 64 * wpr * 8 floats.
@@ -63,14 +70,17 @@ size_t bwd_tree_lds(int gpb, int nv, int wpr) {
 }
 
 // Block count P of the backward pass with a weight gradient (= rows of the [P, n] partials):
-// one block per gpb rows, at most 256 (one 1024-thread block per CU), at least 1. Only
-// (rows, n) enter, so the weight-gradient summation order is fixed for a shape.
+// one block per gpb rows, at least 1, at most 256 (one block per CU, each row group taking
+// several rows) or, from 2^26 elements on, 512 (two blocks per CU: at config 5 247 us against
+// 297 with 256; at config 4 P = 512 costs 20.8 us against 19.2). Only (rows, n) enter, so the
+// weight-gradient summation order is fixed for a shape.
 int64_t bwd_partials(int64_t rows, int64_t n) {
   int wpr, nv;
   norm_shape(n, &wpr, &nv);
   const int64_t gpb = bwd_groups(wpr);
+  const int64_t cap = rows * n >= (int64_t{1} << 26) ? 512 : 256;
   int64_t p = (rows + gpb - 1) / gpb;
-  if (p > 256) p = 256;
+  if (p > cap) p = cap;
   return p < 1 ? 1 : p;
 }
 

@@ -73,7 +73,7 @@ struct BwdArgs {
 
 constexpr int kFwdMaxThreads = 1024;
 constexpr int kMaxNV = 3;
-constexpr int kBwdThreads = 1024;
+constexpr int kBwdThreads = 1024;  // largest backward block (the launch picks its size)
 constexpr int kMaxDy = 5;
 
 // Sum of x over the wavefronts of this row group. `red` holds one float per wavefront.

@@ -112,10 +112,10 @@ def test_rope_validation():
 @pytest.mark.parametrize("rows,n", [(1, 1536), (37, 1536), (8192, 1536), (65536, 3584),
                                     (4557, 1536), (100000, 24), (8192, 16384)])
 def test_partition_depends_on_shape_only(rows, n):
-    """The weight-gradient partition: at most 256 partial rows, every row covered, and a
-    pure function of (rows, n) (the C ABI takes no device argument)."""
+    """The weight-gradient partition: at most 256 partial rows (512 from 2^26 elements on),
+    every row covered, and a pure function of (rows, n) (the C ABI takes no device argument)."""
     p = _hip.rmsnorm_partials(rows, n)
-    assert 1 <= p <= 256 and p == _hip.rmsnorm_partials(rows, n)
+    assert 1 <= p <= (512 if rows * n >= 1 << 26 else 256) and p == _hip.rmsnorm_partials(rows, n)
     assert _hip.rmsnorm_partials(0, n) == 0
 
 
