@@ -209,3 +209,21 @@ def test_nf4_dequant_multi_validation():
     assert call(out=None) == -1 and b"weight 1" in lib.esep_last_error()
     assert call(n_blocks=-1) == -2
     assert call(packed=68) == -3 and call(out=72) == -3
+
+
+def test_apply_installs_the_patches_idempotently():
+    """solution.apply() (the reference's entry, solution/__init__.py:19-25) patches Qwen2MLP and
+    Qwen2Model once; a second call changes nothing. CPU only: no kernel runs."""
+    import solution
+    from transformers.models.qwen2 import modeling_qwen2 as mq
+
+    mlp0, model0 = mq.Qwen2MLP.forward, mq.Qwen2Model.forward
+    try:
+        solution.apply()
+        mlp1, model1 = mq.Qwen2MLP.forward, mq.Qwen2Model.forward
+        assert getattr(mlp1, "_esep_swiglu", False) and mlp1.__wrapped__ is mlp0
+        assert model1 is not model0
+        solution.apply()
+        assert mq.Qwen2MLP.forward is mlp1 and mq.Qwen2Model.forward is model1
+    finally:
+        mq.Qwen2MLP.forward, mq.Qwen2Model.forward = mlp0, model0
