@@ -29,7 +29,9 @@ from ..body import _hip
 # Rows per chunk (reference op.py:34 uses 256). The chunk buffer is [CHUNK_ROWS, V] in the
 # weight's dtype: 4096 x 151936 x 2 B = 1.16 GiB, small against the 288 GB of an MI355X. On
 # MI355X (Qwen2.5 head, 8192 rows, forward + dX) 4096-row chunks take 7.9 ms against 21.6 ms
-# with 256: the two GEMMs need the larger M to fill 256 CUs.
+# with 256: the two GEMMs need the larger M to fill 256 CUs. (One 8192-row chunk measured 8.0 ms
+# with every row weighted but 9.0 ms with every 7th row ignored: the dX GEMM then runs at
+# M = 7021, for which hipBLASLt picks a slower kernel than for 4096 + 2925.)
 CHUNK_ROWS = 4096
 # g = (softmax - onehot) * G_SCALE in fp16 keeps small probabilities out of the fp16 subnormal
 # range (reference op.py:36); undone in fp32 after the g @ W GEMM.
