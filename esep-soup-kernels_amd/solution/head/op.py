@@ -16,8 +16,9 @@ row kernel replaced by esep_head_row_softmax.
 Per chunk of rows (reference op.py:63-93): z = x_c W^T by hipBLASLt (logits in the weight's
 dtype, fp32 accumulation) into one reused [chunk, V] buffer; esep_head_row_softmax computes the
 row statistics and overwrites the weighted rows with g = (softmax - onehot) * G_SCALE in place;
-dX_c = g W by hipBLASLt with fp32 output, for the weighted rows only, scaled by
-ce_weight / G_SCALE in fp32. Rows that carry a loss are moved to the front first (stable), so
+dX_c = g W by hipBLASLt with fp32 output, for the weighted rows only (computed over the whole
+chunk when at least half of it is weighted: a faster GEMM shape), scaled by ce_weight / G_SCALE
+in fp32. Rows that carry a loss are moved to the front first (stable), so
 the g pass and the second GEMM run on a prefix. dX is computed in the forward (when a gradient
 is wanted) and the backward only scales it by the incoming gradient.
 """
@@ -61,6 +62,7 @@ def _run(x16, w16, target, cew, n_live, need_grad, chunk_rows=CHUNK_ROWS):
     dx = torch.zeros(n, h, device=dev, dtype=torch.float32) if need_grad else None
     nc = max(1, min(chunk_rows, n))
     z = torch.empty(nc, v, device=dev, dtype=w16.dtype)
+    dxt = None
     wt = w16.t()
     for r0 in range(0, n, nc):
         nr = min(nc, n - r0)
@@ -71,9 +73,20 @@ def _run(x16, w16, target, cew, n_live, need_grad, chunk_rows=CHUNK_ROWS):
                               need_grad, G_SCALE)
         nl = min(max(n_live - r0, 0), nr)
         if need_grad and nl:
-            dxc = dx[r0:r0 + nl]
-            torch.mm(zc[:nl], w16, out_dtype=torch.float32, out=dxc)
-            dxc.mul_((cew[r0:r0 + nl] * (1.0 / G_SCALE))[:, None])
+            scale = (cew[r0:r0 + nl] * (1.0 / G_SCALE))[:, None]
+            if 2 * nl >= nc and nl < nc:
+                # hipBLASLt runs this GEMM much faster at the chunk's row count than at a ragged
+                # count of weighted rows (MI355X, K = 151936, N = 1536: M = 2925 2.06 ms,
+                # M = 4096 1.67 ms), so it covers the whole chunk buffer and the rows past the
+                # weighted ones (logits, or a previous chunk's rows) are computed and dropped
+                if dxt is None:
+                    dxt = torch.empty(nc, h, device=dev, dtype=torch.float32)
+                torch.mm(z, w16, out_dtype=torch.float32, out=dxt)
+                torch.mul(dxt[:nl], scale, out=dx[r0:r0 + nl])
+            else:
+                dxc = dx[r0:r0 + nl]
+                torch.mm(zc[:nl], w16, out_dtype=torch.float32, out=dxc)
+                dxc.mul_(scale)
     return lse, tlogit, ent, amax, dx
 
 
