@@ -24,7 +24,11 @@ namespace {
 
 constexpr int kSwThreads = 256;
 
-__device__ __forceinline__ float sigmoid_f(float g) { return 1.f / (1.f + expf(-g)); }
+// sigmoid on the hardware's v_exp_f32 and v_rcp_f32 (each ~1 ulp; no denormal-range or
+// division fix-ups: the kernels are memory-bound and keep their VALU work small)
+__device__ __forceinline__ float sigmoid_f(float g) {
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(g * -1.4426950408889634f));
+}
 
 template <typename T>
 __device__ __forceinline__ void ld8(const T* p, float (&v)[8]) {
