@@ -241,6 +241,27 @@ def run_config5(dev, steps):
             "kernels": kernels}
 
 
+def run_config4_other_rstd(dev, steps, save_rstd):
+    """Config 4's step graph with the other rstd mode (saved by the forward and read by the
+    backward, or recomputed from x in the backward); returns the JSON object."""
+    import torch
+
+    body = Body(CFG4, save_rstd, dev)
+    torch.cuda.synchronize()
+    g = capture(body.step)
+    time_graph(g, 2)
+    ev_ms, wall_ms = time_graph(g, steps)
+    ms = max(ev_ms, wall_ms)
+    nbytes = body.step_bytes()
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    mode = "saved" if save_rstd else "recomputed"
+    log(f"config 4, rstd {mode}: {ms:.3f} ms per step, {gbs:.0f} GB/s = {gbs / PEAK_GBS:.1%} of peak")
+    del g, body
+    torch.cuda.empty_cache()
+    return {"rstd": mode, "ms_per_step": round(ms, 4), "GB/s": round(gbs, 1),
+            "frac_of_peak": round(gbs / PEAK_GBS, 4), "bytes_per_step": nbytes}
+
+
 def capture(fn, warm=True):
     import torch
 
@@ -746,6 +767,7 @@ def main():
     del g
     del body
     torch.cuda.empty_cache()
+    c4_other = run_config4_other_rstd(dev, max(args.steps // 3, 5), not save_rstd)
     c5 = None if args.no_config5 else run_config5(dev, max(args.steps // 3, 5))
     api = run_api_variant(dev, max(args.steps // 3, 5))
     attn = None if args.no_attention else run_attention(dev, max(args.steps // 3, 5))
@@ -778,6 +800,7 @@ def main():
         "ms_per_step_events": round(ev_ms, 4),
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "config4_other_rstd": c4_other,
         "config5": c5,
         "api_variant": api,
         "attention": attn,
