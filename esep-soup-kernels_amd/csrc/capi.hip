@@ -152,6 +152,7 @@ int esep_rmsnorm_fwd(const void* x, int x_dt, int64_t ld_x, const void* delta, i
   a.vec = vec ? 1 : 0;
 
   const int gpb = wpr >= 4 ? 1 : 4 / wpr;
+  a.gpb = gpb;
   const dim3 block(gpb * 64 * wpr);
   const int64_t blocks = (rows + gpb - 1) / gpb;
   if (blocks > 0x7fffffff) return fail(ESEP_ESHAPE, "rmsnorm_fwd: too many rows");
@@ -242,6 +243,7 @@ int esep_rmsnorm_bwd(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
   // Without a weight gradient every row group owns one row and small blocks (4 row groups of
   // one wavefront, or one group of wpr wavefronts) let finished waves be replaced one by one.
   const int gpb = part ? bwd_groups(wpr) : (wpr >= 4 ? 1 : 4 / wpr);
+  a.gpb = gpb;
   const int64_t blocks = part ? bwd_partials(rows, n) : (rows + gpb - 1) / gpb;
   if (blocks > 0x7fffffff) return fail(ESEP_ESHAPE, "rmsnorm_bwd: too many rows");
 

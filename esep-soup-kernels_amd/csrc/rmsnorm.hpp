@@ -44,6 +44,7 @@ struct FwdArgs {
   int n_special;
   float eps;
   int wpr;  // wavefronts per row
+  int gpb;  // row groups per block (blockDim.x / (64 * wpr))
   int vec;  // 1: every chunk is a whole 16-byte aligned vector
 };
 
@@ -68,6 +69,7 @@ struct BwdArgs {
   int n;
   float eps;
   int wpr;
+  int gpb;  // row groups per block (blockDim.x / (64 * wpr))
   int vec;
 };
 
@@ -121,7 +123,7 @@ __device__ __forceinline__ Span row_rsrc(const void* base, int64_t row, int64_t 
 template <int NV, bool VEC, typename TX, typename TD, typename TY>
 __device__ __forceinline__ void fwd_rows(const FwdArgs& a, float* red) {
   const int G = kWave * a.wpr;
-  const int gpb = blockDim.x / G;
+  const int gpb = a.gpb;  // blockDim.x would cost a vector load of the hidden kernel arguments
   const int grp = wave_id() / a.wpr;
   const int tg = (int)threadIdx.x - grp * G;
   const int64_t row = (int64_t)blockIdx.x * gpb + grp;
@@ -235,7 +237,7 @@ __device__ __forceinline__ void dw_block_partial(const BwdArgs& a, float (&acc)[
 template <int NV, bool VEC, typename TX, typename TDY, typename TO>
 __device__ __forceinline__ void bwd_rows(const BwdArgs& a, float* red, float* lds) {
   const int G = kWave * a.wpr;
-  const int gpb = blockDim.x / G;
+  const int gpb = a.gpb;  // blockDim.x would cost a vector load of the hidden kernel arguments
   const int grp = wave_id() / a.wpr;
   const int tg = (int)threadIdx.x - grp * G;
   const int n = a.n;
@@ -398,7 +400,7 @@ __device__ __forceinline__ void bwd_rows(const BwdArgs& a, float* red, float* ld
 template <int NV, typename TX, typename TDY, typename TO>
 __device__ __forceinline__ void bwd_rows_fast(const BwdArgs& a, float* red, float* lds) {
   const int G = kWave * a.wpr;
-  const int gpb = blockDim.x / G;
+  const int gpb = a.gpb;  // blockDim.x would cost a vector load of the hidden kernel arguments
   const int grp = wave_id() / a.wpr;
   const int tg = (int)threadIdx.x - grp * G;
   const int n = a.n;
@@ -410,7 +412,7 @@ __device__ __forceinline__ void bwd_rows_fast(const BwdArgs& a, float* red, floa
   const int stride = NV * G * 8;  // floats per slot (>= n; the tail past n stays 0)
   float* acc = lds + grp * stride;
   float* wl = lds + (want_dw ? gpb * stride : 0);
-  for (int q = threadIdx.x; q < stride / 4; q += blockDim.x) {
+  for (int q = threadIdx.x; q < stride / 4; q += gpb * G) {
     f32x4 t = {0.f, 0.f, 0.f, 0.f};
     if (4 * q < n) t = *reinterpret_cast<const f32x4*>(a.w + 4 * q);
     *reinterpret_cast<f32x4*>(wl + 4 * q) = t;
@@ -494,7 +496,7 @@ __device__ __forceinline__ void bwd_rows_fast(const BwdArgs& a, float* red, floa
     // block sum: column quads over all threads, groups added in group order
     __syncthreads();
     float* dst = a.part + (int64_t)blockIdx.x * n;
-    for (int q = threadIdx.x; 4 * q < n; q += blockDim.x) {
+    for (int q = threadIdx.x; 4 * q < n; q += gpb * G) {
       f32x4 t = *reinterpret_cast<const f32x4*>(lds + 4 * q);
       for (int g = 1; g < gpb; ++g) t += *reinterpret_cast<const f32x4*>(lds + g * stride + 4 * q);
       *reinterpret_cast<f32x4*>(dst + 4 * q) = t;
