@@ -10,8 +10,9 @@
 //
 // Forward mapping (flash-attention style, one pass, online softmax). A block of 4 wavefronts
 // owns 128 queries of one sequence and one query head; wavefront w owns queries 32w..32w+31 of
-// the block. Keys are staged in tiles of 64 (the tiles the causal mask leaves) and consumed in
-// halves of 32, heaviest query tiles first. Scores are computed transposed, S^T = K Q^T, with
+// the block, heaviest query tiles first. At D = 128 the keys come in tiles of 32 moved by LDS
+// DMA through a two-buffer ring (the next tile in flight during the current one); at D = 64 in
+// tiles of 64 staged through registers and consumed in halves of 32. Scores are computed transposed, S^T = K Q^T, with
 // v_mfma_f32_32x32x16 (K from LDS as the A operand, the wave's Q held in registers as the B
 // operand), so each lane owns one query and 16 of a half's 32 scores; the other 16 sit in lane
 // l ^ 32, and a row max or sum is a register reduction plus one cross-half exchange. The probabilities go straight from the
@@ -140,6 +141,22 @@ __device__ __forceinline__ V ld_tr(const T* M, int r0, int c0, int lane) {
   const s16x4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr)(p + 8 * P));
   return __builtin_bit_cast(V, __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7));
 }
+
+// One LDS DMA instruction: lane l reads the dword at g (its own address) and the wavefront
+// writes the 64 dwords to LDS bytes lds .. lds + 255 (lane l at lds + 4 l). Issued from asm so
+// that the compiler does not track it: its own LDS-DMA tracking cannot tell the two buffers
+// apart for the transposing reads and would wait for the next tile before reading this one.
+// The kernel waits for the DMA itself (s_waitcnt vmcnt(0) before the barrier that publishes a
+// tile). M0 is written right before the load that reads it; the compiler sets M0 afresh before
+// each of its own uses.
+__device__ __forceinline__ void lds_dma_dword(const void* g, const void* lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(m) : "memory");
+}
+
+// s_waitcnt vmcnt(0) (expcnt, lgkmcnt left at their maxima): through the builtin, so that the
+// compiler's own wait tracking sees it too.
+constexpr int kWaitVm0 = 0x0F70;
 
 // Sequence s's token range [start, end), clamped into [0, T].
 __device__ __forceinline__ void seq_bounds(const int32_t* cu, int s, int64_t T, int* start,

@@ -13,9 +13,10 @@
 // k_attn_bwd_dkdv: one block per (256 keys at D = 128, 128 at D = 64; kv head; part of the kv
 // head's query heads); wavefront w owns keys 32w..32w+31 and holds their K in registers as B
 // operands (V's come from the block's V rows in LDS). It
-// walks, for each of its query heads in turn and each query tile of 64 at or after its keys
-// (the next tile prefetched into registers during the current one), S = Q K^T and dP = dO V^T (Q and dO
-// staged row-major in LDS as A operands), then dV^T += dO^T P and dK^T += Q^T dS (Q^T and dO^T
+// walks, for each of its query heads in turn and each query tile at or after its keys (at
+// D = 128 the next tile's Q / dO / lse / delta moved by LDS DMA into the other buffer of a
+// two-buffer ring during the current one; at D = 64 prefetched into registers), S = Q K^T and
+// dP = dO V^T (Q and dO row-major in LDS as A operands), then dV^T += dO^T P and dK^T += Q^T dS (Q^T and dO^T
 // read transposed out of the same tiles, P and dS from registers in the permuted query order). Each key's dK and
 // dV are summed by one lane in a fixed order over heads and query tiles; with the heads split
 // over several blocks (short inputs, to fill the GPU), each part writes fp32 partials and
@@ -153,10 +154,15 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs 
   using V8 = typename Mfma<T>::v8;
   const AttnArgs& a = b.f;
   constexpr int RP = D + kRowPad;  // row-major pitch
-  __shared__ __align__(16) T qs[BQ * RP];   // Q row-major (A operand of S; transposed, of dK^T)
-  __shared__ __align__(16) T ds_[BQ * RP];  // dO row-major (A operand of dP; transposed, of dV^T)
-  __shared__ __align__(16) float lse_s[BQ];
-  __shared__ __align__(16) float del_s[BQ];
+  // DMA (D = 128): the Q / dO / lse / delta of a work item move by LDS DMA into a ring of two
+  // buffers, item it + 1 in flight while item it is consumed, one barrier per item; query rows
+  // past the sequence end repeat its last row and are masked (p = 0). Otherwise (D = 64: rows of
+  // 128 bytes) they move through registers, the next item prefetched, rows past the end zeroed.
+  constexpr bool DMA = D == 128;
+  constexpr int NB = DMA ? 2 : 1;
+  __shared__ __align__(16) T qs[NB][BQ * RP];   // Q row-major (A operand of S; transposed, of dK^T)
+  __shared__ __align__(16) T ds_[NB][BQ * RP];  // dO row-major (A operand of dP; transposed, of dV^T)
+  __shared__ __align__(16) float ld_s[NB][2 * BQ];  // lse (log2 units without DMA), then delta
   __shared__ __align__(16) T vsm[BK * RP];  // this block's V rows (B operands of dP)
 
   const int seq = blockIdx.z;
@@ -194,10 +200,10 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs 
 #pragma unroll
   for (int md = 0; md < D / 32; ++md) dka[md] = dva[md] = f32x16{};
 
-  // Work items (head, query tile) in order; the next item's Q, dO, lse and delta are loaded
-  // into registers while the current one is computed.
+  // Work items (head, query tile) in order.
   const int nqt = (end - k0 + BQ - 1) / BQ;
   const int items = gs * nqt;
+  // register path: the next item's Q, dO, lse and delta, loaded while the current one is computed
   TileRows<T, D, BQ, NT> pq, pd;
   float lse_n = 0.f, del_n = 0.f;
   auto prefetch = [&](int it) {
@@ -211,28 +217,75 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs 
       del_n = t < end ? b.delta[(int64_t)h * a.T + t] : 0.f;
     }
   };
-  if (items > 0) prefetch(0);
+  // DMA path: wavefront w moves rows w, w + NW, ... of Q and dO (one 256-byte row per
+  // instruction) and wavefront 0 the lse / delta words (64 per instruction)
+  const int wu = __builtin_amdgcn_readfirstlane(w);
+  auto issue = [&](int it, int buf) {
+    const int h = h0 + it / nqt, qt = k0 + (it % nqt) * BQ;
+    const int64_t col = (int64_t)h * D;
+#pragma unroll
+    for (int jj = 0; jj < BQ / NW; ++jj) {
+      const int j = NW * jj + wu;
+      const int r = qt + j < end ? qt + j : end - 1;
+      lds_dma_dword(reinterpret_cast<const uint32_t*>(static_cast<const T*>(a.q) + (int64_t)r * a.q_rs + col) + lane,
+                    &qs[buf][j * RP]);
+      lds_dma_dword(reinterpret_cast<const uint32_t*>(static_cast<const T*>(b.dout) + (int64_t)r * b.do_rs + col) + lane,
+                    &ds_[buf][j * RP]);
+    }
+    if (wu == 0) {
+#pragma unroll
+      for (int k = 0; k < 2 * BQ / 64; ++k) {
+        const int f = 64 * k + lane;  // word f of [lse | delta]
+        const int t0 = qt + (f < BQ ? f : f - BQ);
+        const int t = t0 < end ? t0 : end - 1;
+        const float* src = (f < BQ ? a.lse : b.delta) + (int64_t)h * a.T + t;
+        lds_dma_dword(src, &ld_s[buf][64 * k]);
+      }
+    }
+  };
+  if (items > 0) {
+    if constexpr (DMA)
+      issue(0, 0);
+    else
+      prefetch(0);
+  }
 
   for (int it = 0; it < items; ++it) {
     const int qt = k0 + (it % nqt) * BQ;
-    __syncthreads();  // the previous item's LDS reads are done
-    pq.template store<RP>(qs, tid);
-    pd.template store<RP>(ds_, tid);
-    if (tid < BQ) {
-      lse_s[tid] = lse_n;
-      del_s[tid] = del_n;
+    const int buf = DMA ? (it & 1) : 0;
+    if constexpr (DMA) {
+      // this wavefront's DMA of item it has landed; the barrier publishes every wavefront's
+      // rows and certifies that item it - 1 (the other buffer) is consumed
+      __builtin_amdgcn_s_waitcnt(kWaitVm0);
+      __syncthreads();
+      if (it + 1 < items) issue(it + 1, buf ^ 1);
+    } else {
+      __syncthreads();  // the previous item's LDS reads are done
+      pq.template store<RP>(qs[0], tid);
+      pd.template store<RP>(ds_[0], tid);
+      if (tid < BQ) {
+        ld_s[0][tid] = lse_n;
+        ld_s[0][BQ + tid] = del_n;
+      }
+      __syncthreads();
+      if (it + 1 < items) prefetch(it + 1);
     }
-    __syncthreads();
-    if (it + 1 < items) prefetch(it + 1);
     // every query of the tile comes before this wave's keys: nothing to add
     if (!wave_live || qt + BQ - 1 < kw0) continue;
+    const T* qsb = qs[buf];
+    const T* dsb = ds_[buf];
+    const float* lse_s = ld_s[buf];
+    const float* del_s = ld_s[buf] + BQ;
+    // with DMA, rows past the sequence end hold repeated data: mask them like future queries
+    const int qlim = DMA ? end : 0x7fffffff;
+    const float lmul = DMA ? kLog2e : 1.f;
 
     // one 32-query half at a time
 #pragma unroll
     for (int qh = 0; qh < BQ / 32; ++qh) {
       f32x16 s = f32x16{}, dp = f32x16{};
-      const T* qrow = &qs[(32 * qh + lq) * RP + 8 * hi];
-      const T* drow = &ds_[(32 * qh + lq) * RP + 8 * hi];
+      const T* qrow = &qsb[(32 * qh + lq) * RP + 8 * hi];
+      const T* drow = &dsb[(32 * qh + lq) * RP + 8 * hi];
 #pragma unroll
       for (int c = 0; c < D / 16; ++c) {
         s = Mfma<T>::run(ld16<V8>(qrow + 16 * c), kb[c], s);
@@ -242,11 +295,11 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs 
       // past the sequence end have Q = dO = 0 (staged as zeros), so they add nothing to dK or
       // dV whatever their p; only the causal mask needs applying, and only on the half-tiles
       // whose first query precedes the wave's last key.
-      if (qt + 32 * qh < kw0 + 31) {
+      if (qt + 32 * qh < kw0 + 31 || qt + 32 * qh + 31 >= qlim) {
 #pragma unroll
         for (int i = 0; i < 16; ++i) {
           const int t = qt + 32 * qh + 8 * (i / 4) + 4 * hi + (i % 4);
-          if (t < kj) s[i] = -INFINITY;
+          if (t < kj || t >= qlim) s[i] = -INFINITY;
         }
       }
       V8 pb[2], sb_[2];
@@ -258,7 +311,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs 
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           const int i = 4 * j + e;
-          const float p = exp2_fast(fmaf(s[i], a.scale_log2, -lr[e]));
+          const float p = exp2_fast(fmaf(s[i], a.scale_log2, -lr[e] * lmul));
           pb[i / 8][i % 8] = (T)p;
           sb_[i / 8][i % 8] = (T)(p * (dp[i] - dr[e]));
         }
@@ -269,8 +322,8 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs 
 #pragma unroll
         for (int c2 = 0; c2 < 2; ++c2) {
           const int rb = 32 * qh + 16 * c2;
-          dva[md] = Mfma<T>::run(ld_tr<V8, RP>(ds_, rb, 32 * md, lane), pb[c2], dva[md]);
-          dka[md] = Mfma<T>::run(ld_tr<V8, RP>(qs, rb, 32 * md, lane), sb_[c2], dka[md]);
+          dva[md] = Mfma<T>::run(ld_tr<V8, RP>(dsb, rb, 32 * md, lane), pb[c2], dva[md]);
+          dka[md] = Mfma<T>::run(ld_tr<V8, RP>(qsb, rb, 32 * md, lane), sb_[c2], dka[md]);
         }
     }
   }

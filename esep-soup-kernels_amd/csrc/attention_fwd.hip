@@ -6,6 +6,69 @@
 namespace esep {
 namespace {
 
+// One 32-key half of the online softmax for a wavefront's 32 queries: keys kh .. kh + 31, held
+// in rows r0 .. r0 + 31 of the row-major LDS tiles ks / vs (pitch KP). Lane (lq, hi) gets the
+// scores of its query qi against keys kh + 8 (i / 4) + 4 hi + i % 4, i < 16, from
+// S^T = K Q^T (K rows from LDS as the A operand, the wave's Q^T in registers as B), then
+// updates (m, l) and O^T += V^T P^T.
+template <typename T, int D, int KP>
+__device__ __forceinline__ void fwd_half(const T* ks, const T* vs, int r0, int kh, int qw0, int qi,
+                                         int lane, float scale_log2,
+                                         const typename Mfma<T>::v8 (&qb)[D / 16],
+                                         f32x16 (&oacc)[D / 32], float& m, float& l) {
+  using V8 = typename Mfma<T>::v8;
+  const int lq = lane & 31, hi = lane >> 5;
+  f32x16 acc = f32x16{};
+  const T* krow = &ks[(r0 + lq) * KP + 8 * hi];
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) acc = Mfma<T>::run(ld16<V8>(krow + 16 * c), qb[c], acc);
+  // the causal mask only bites on the half-tiles that reach past the wave's first query
+  if (kh + 31 > qw0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int kj = kh + 8 * (i / 4) + 4 * hi + (i % 4);
+      if (kj > qi) acc[i] = -INFINITY;
+    }
+  }
+  float mx = acc[0];
+#pragma unroll
+  for (int i = 1; i < 16; ++i) mx = fmaxf(mx, acc[i]);
+  mx = pair_max(mx) * scale_log2;
+  // Online softmax (base 2) with a lazy reference: the lane's m moves only when the half's
+  // maximum exceeds it by more than 8, so p <= 2^8 (exact in bf16 / fp16 relative terms) and
+  // O, l are rescaled only in the rare half-tiles where some lane's m moved.
+  const bool grow = mx > m + 8.f;
+  float alpha = 1.f;
+  if (grow) {
+    alpha = exp2_fast(m - mx);  // m = -inf on the first half: alpha = 0, O and l are 0
+    m = mx;
+  }
+  const float nm = m == -INFINITY ? 0.f : -m;  // a lane with no visible key yet: p = 0
+  float ps = 0.f;
+  V8 pb[2];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float p = exp2_fast(fmaf(acc[i], scale_log2, nm));
+    ps += p;
+    pb[i / 8][i % 8] = (T)p;
+  }
+  ps = pair_sum(ps);
+  l = fmaf(l, alpha, ps);
+  if (__any(grow)) {
+#pragma unroll
+    for (int md = 0; md < D / 32; ++md) oacc[md] *= alpha;
+  }
+  // O^T += V^T P^T over the 32 keys, contraction in the permuted key order of pb (element e of
+  // chunk c2 is key kh + 16 c2 + 8 (e / 4) + 4 hi + e % 4); V^T read transposed out of the
+  // row-major V tile.
+#pragma unroll
+  for (int md = 0; md < D / 32; ++md)
+#pragma unroll
+    for (int c2 = 0; c2 < 2; ++c2)
+      oacc[md] = Mfma<T>::run(ld_tr<V8, KP>(vs, r0 + 16 * c2, 32 * md, lane), pb[c2], oacc[md]);
+}
+
+// The D = 64 forward: K / V staged through registers in 64-key tiles (rows of 128 bytes).
 template <typename T, int D>
 // 3 wavefronts per SIMD (<= 168 registers): without the bound the compiler parks the
 // accumulators in AGPRs and stops at 2.
@@ -61,62 +124,11 @@ __global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd(const AttnArgs a) 
     __syncthreads();
     if (!wave_live || kt > wq_last) continue;  // every key of the tile is after this wave's queries
 
-    // One 32-key half at a time: scores, online-softmax update, then P V for that half.
-    // (Keeping both halves' scores live needs ~250 registers, 2 wavefronts per SIMD; one half
-    // at a time fits 3, which measured a third faster.) Lane (lq, hi) gets the scores of query
-    // qi against keys kt + 32 sb + 8 (i / 4) + 4 hi + i % 4, i < 16.
+    // One 32-key half at a time: keeping both halves' scores live needs ~250 registers,
+    // 2 wavefronts per SIMD; one half at a time fits 3, which measured a third faster.
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-      f32x16 acc = f32x16{};
-      const T* krow = &ks[(32 * sb + lq) * KP + 8 * hi];
-#pragma unroll
-      for (int c = 0; c < D / 16; ++c) acc = Mfma<T>::run(ld16<V8>(krow + 16 * c), qb[c], acc);
-      // the causal mask only bites on the half-tiles that reach past the wave's first query
-      if (kt + 32 * sb + 31 > qw0) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int kj = kt + 32 * sb + 8 * (i / 4) + 4 * hi + (i % 4);
-          if (kj > qi) acc[i] = -INFINITY;
-        }
-      }
-      float mx = acc[0];
-#pragma unroll
-      for (int i = 1; i < 16; ++i) mx = fmaxf(mx, acc[i]);
-      mx = pair_max(mx) * a.scale_log2;
-      // Online softmax (base 2) with a lazy reference: the lane's m moves only when the half's
-      // maximum exceeds it by more than 8, so p <= 2^8 (exact in bf16 / fp16 relative terms)
-      // and O, l are rescaled only in the rare half-tiles where some lane's m moved.
-      const bool grow = mx > m + 8.f;
-      float alpha = 1.f;
-      if (grow) {
-        alpha = exp2_fast(m - mx);  // m = -inf on the first half: alpha = 0, O and l are 0
-        m = mx;
-      }
-      const float nm = m == -INFINITY ? 0.f : -m;  // a lane with no visible key yet: p = 0
-      float ps = 0.f;
-      V8 pb[2];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float p = exp2_fast(fmaf(acc[i], a.scale_log2, nm));
-        ps += p;
-        pb[i / 8][i % 8] = (T)p;
-      }
-      ps = pair_sum(ps);
-      l = fmaf(l, alpha, ps);
-      if (__any(grow)) {
-#pragma unroll
-        for (int md = 0; md < D / 32; ++md) oacc[md] *= alpha;
-      }
-      // O^T += V^T P^T over the 32 keys, contraction in the permuted key order of pb (element
-      // e of chunk c2 is key 32 sb + 16 c2 + 8 (e / 4) + 4 hi + e % 4); V^T read transposed out
-      // of the row-major V tile.
-#pragma unroll
-      for (int md = 0; md < D / 32; ++md)
-#pragma unroll
-        for (int c2 = 0; c2 < 2; ++c2)
-          oacc[md] = Mfma<T>::run(ld_tr<V8, KP>(vs, 32 * sb + 16 * c2, 32 * md, lane), pb[c2],
-                                  oacc[md]);
-    }
+    for (int sb = 0; sb < 2; ++sb)
+      fwd_half<T, D, KP>(ks, vs, 32 * sb, kt + 32 * sb, qw0, qi, lane, a.scale_log2, qb, oacc, m, l);
   }
 
   if (!wave_live || qi >= end) return;
@@ -127,11 +139,93 @@ __global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd(const AttnArgs a) 
     a.lse[(int64_t)h * a.T + qi] = (m + log2f(l)) * 0.69314718055994531f;
 }
 
+// D = 128 forward with the K / V tiles moved by LDS DMA (lds_dma_dword: one 256-byte token row
+// per instruction, straight into LDS, no registers) in tiles of 32 keys through a ring of two
+// buffers: tile t + 1 is in flight while tile t is consumed, and one barrier per tile both
+// publishes tile t and certifies that tile t - 1 is consumed, freeing its buffer. Rows keep the
+// padded pitch, so the operand reads stay conflict-free; rows past kend repeat row kend - 1
+// (finite data; every such key is masked, so it contributes p = 0). 39 KiB of LDS per block:
+// 3 blocks per CU, as the registers allow. Measured at config 5 against the register-staged
+// kernel (64-key tiles, two barriers per tile): 2.13 -> 2.01 ms; 64-key tiles in the ring
+// (2 blocks per CU) 2.79 ms, a ring of three 32-key tiles at a 68-dword pitch 2.23 ms.
+template <typename T>
+__global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd_dma(const AttnArgs a) {
+  constexpr int D = 128;
+  constexpr int BN = 32;
+  using V8 = typename Mfma<T>::v8;
+  constexpr int KP = D + kRowPad;
+  __shared__ __align__(16) T kv[2][2][BN * KP];  // [buffer][K, V][row-major tile]
+
+  const int seq = blockIdx.z, h = blockIdx.y;
+  int start, end;
+  seq_bounds(a.cu, seq, a.T, &start, &end);
+  const int ntiles_q = (end - start + kAttnBM - 1) / kAttnBM;
+  if ((int)blockIdx.x >= ntiles_q) return;
+  const int q0 = start + (ntiles_q - 1 - (int)blockIdx.x) * kAttnBM;  // heaviest tiles first
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq = lane & 31, hi = lane >> 5;
+  const int kvh = h / (a.HQ / a.HK);
+  const int qw0 = q0 + 32 * w;
+  const int qi = qw0 + lq;
+  const bool wave_live = qw0 < end;
+  const int wq_last = qw0 + 31 < end ? qw0 + 31 : end - 1;
+
+  V8 qb[D / 16];
+  {
+    const T* qrow = static_cast<const T*>(a.q) + (int64_t)qi * a.q_rs + (int64_t)h * D + 8 * hi;
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c)
+      qb[c] = qi < end ? ld16<V8>(qrow + 16 * c) : V8{};
+  }
+
+  f32x16 oacc[D / 32];
+#pragma unroll
+  for (int md = 0; md < D / 32; ++md) oacc[md] = f32x16{};
+  float m = -INFINITY, l = 0.f;
+  const int kend = end < q0 + kAttnBM ? end : q0 + kAttnBM;
+  const T* kbase = static_cast<const T*>(a.k) + (int64_t)kvh * D;
+  const T* vbase = static_cast<const T*>(a.v) + (int64_t)kvh * D;
+  const int ntiles = (kend - start + BN - 1) / BN;
+
+  // wavefront w moves rows w, w + 4, ... of the tile's K and V
+  auto issue = [&](T* kd, T* vd, int kt) {
+#pragma unroll
+    for (int jj = 0; jj < BN / 4; ++jj) {
+      const int j = 4 * jj + w;
+      const int r = kt + j < kend ? kt + j : kend - 1;
+      lds_dma_dword(reinterpret_cast<const uint32_t*>(kbase + (int64_t)r * a.k_rs) + lane, kd + j * KP);
+      lds_dma_dword(reinterpret_cast<const uint32_t*>(vbase + (int64_t)r * a.v_rs) + lane, vd + j * KP);
+    }
+  };
+
+  auto consume = [&](const T* ks, const T* vs, int kt) {
+    if (!wave_live || kt > wq_last) return;  // every key of the tile is after this wave's queries
+    fwd_half<T, D, KP>(ks, vs, 0, kt, qw0, qi, lane, a.scale_log2, qb, oacc, m, l);
+  };
+
+  if (ntiles > 0) issue(kv[0][0], kv[0][1], start);
+  for (int t = 0; t < ntiles; ++t) {
+    // this wavefront's DMA of tile t has landed; the barrier publishes every wavefront's rows
+    // and certifies that tile t - 1, in the other buffer, is consumed
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __syncthreads();
+    if (t + 1 < ntiles) issue(kv[(t + 1) & 1][0], kv[(t + 1) & 1][1], start + (t + 1) * BN);
+    consume(kv[t & 1][0], kv[t & 1][1], start + t * BN);
+  }
+
+  if (!wave_live || qi >= end) return;
+  store_rows_t<T, D>(static_cast<T*>(a.o) + (int64_t)qi * a.o_rs + (int64_t)h * D, oacc, hi,
+                     l > 0.f ? 1.f / l : 0.f);
+  if (hi == 0 && a.lse != nullptr)
+    a.lse[(int64_t)h * a.T + qi] = (m + log2f(l)) * 0.69314718055994531f;
+}
+
 template <typename T>
 hipError_t fwd_d(const AttnArgs& a, int D, dim3 grid, hipStream_t s, bool* sup) {
   *sup = true;
   if (D == 128)
-    hipLaunchKernelGGL((k_attn_fwd<T, 128>), grid, dim3(kAttnThreads), 0, s, a);
+    hipLaunchKernelGGL((k_attn_fwd_dma<T>), grid, dim3(kAttnThreads), 0, s, a);
   else if (D == 64)
     hipLaunchKernelGGL((k_attn_fwd<T, 64>), grid, dim3(kAttnThreads), 0, s, a);
   else {
