@@ -146,15 +146,18 @@ def test_attn_bwd_deterministic():
     assert all(torch.equal(a, b) for a, b in zip(*runs))
 
 
-def test_attn_bwd_long_sequences_sampled_keys():
-    """A config-5-like shape (4 sequences of 4096, 28 / 4 heads, D = 128: enough key blocks that
+@pytest.mark.parametrize("lengths", [[4096] * 4, [4000, 4097, 3999, 4100]], ids=["even", "ragged"])
+def test_attn_bwd_long_sequences_sampled_keys(lengths):
+    """A config-5-like shape (4 sequences of ~4096, 28 / 4 heads, D = 128: enough key blocks that
     the kernel does not split the query heads, so the 4-wavefront dK / dV kernel runs) checked on
     sampled keys against float64 sums restated from the formulas (dV_j = sum_q P_qj dO_q,
     dK_j = scale sum_q P_qj (dP_qj - delta_q) Q_q over the causal queries of every query head of
-    the kv head), with the kernel's own lse and O for P and delta."""
+    the kv head), with the kernel's own lse and O for P and delta. The ragged lengths put the
+    end of every sequence inside a query tile (rows past the end staged and masked); the sample
+    takes keys from the last 40 tokens of each sequence as well as from anywhere."""
     from solution.body import _hip
 
-    lengths, HQ, HK, D = [4096] * 4, 28, 4, 128
+    HQ, HK, D = 28, 4, 128
     q, k, v, cu = _inputs(lengths, HQ, HK, D, torch.bfloat16, seed=31)
     T = q.shape[0]
     assert ((T + 255) // 256) * HK >= 256  # no split: the 4-wavefront kernel
@@ -162,16 +165,19 @@ def test_attn_bwd_long_sequences_sampled_keys():
     scale = D ** -0.5
     o = torch.empty_like(q)
     lse = torch.empty((HQ, T), device=DEV)
-    _hip.attn_fwd(q, k, v, o, cu, 4096, scale, lse=lse)
+    L_max = max(lengths)
+    _hip.attn_fwd(q, k, v, o, cu, L_max, scale, lse=lse)
     dq, dk, dv = torch.empty_like(q), torch.empty_like(k), torch.empty_like(v)
-    _hip.attn_bwd(q, k, v, o, do, lse, dq, dk, dv, cu, 4096, scale)
+    _hip.attn_bwd(q, k, v, o, do, lse, dq, dk, dv, cu, L_max, scale)
     Q, K, V, DO, O, L = (np64(t) for t in (q, k, v, do, o, lse))
     DK, DV = np64(dk), np64(dv)
     G = HQ // HK
+    bounds = np.concatenate([[0], np.cumsum(lengths)])
     rng = np.random.default_rng(33)
-    for j in sorted(rng.choice(T, 24, replace=False)):
-        s0 = (j // 4096) * 4096
-        t = np.arange(j, s0 + 4096)  # causal queries of key j
+    tails = [int(rng.integers(e - 40, e)) for e in bounds[1:]]
+    for j in sorted(set(rng.choice(T, 20, replace=False).tolist() + tails)):
+        s_end = bounds[np.searchsorted(bounds, j, side="right")]
+        t = np.arange(j, s_end)  # causal queries of key j
         for hk in range(HK):
             gdk = np.zeros(D)
             gdv = np.zeros(D)
