@@ -20,8 +20,27 @@ __device__ __forceinline__ void fwd_half(const T* ks, const T* vs, int r0, int k
   const int lq = lane & 31, hi = lane >> 5;
   f32x16 acc = f32x16{};
   const T* krow = &ks[(r0 + lq) * KP + 8 * hi];
+  // K operands read three ahead of the MFMA that uses them; the scheduling barriers keep the
+  // compiler from sinking each read to just before its use (two ahead), which left an LDS
+  // round trip exposed per pair of MFMAs (config 5 forward 2.03 -> 1.98 ms)
+  constexpr int KA = 3;
+  V8 kbuf[KA];
 #pragma unroll
-  for (int c = 0; c < D / 16; ++c) acc = Mfma<T>::run(ld16<V8>(krow + 16 * c), qb[c], acc);
+  for (int c = 0; c < KA; ++c) kbuf[c] = ld16<V8>(krow + 16 * c);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) {
+    acc = Mfma<T>::run(kbuf[c % KA], qb[c], acc);
+    if (c + KA < D / 16) kbuf[c % KA] = ld16<V8>(krow + 16 * (c + KA));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // the first two V^T operands (PV order j = 2 md + c2) read before the softmax, whose VALU
+  // work hides their LDS latency (1.98 -> 1.93 ms)
+  constexpr int VA = 2;
+  V8 vbuf[VA];
+#pragma unroll
+  for (int j = 0; j < VA; ++j) vbuf[j] = ld_tr<V8, KP>(vs, r0 + 16 * (j % 2), 32 * (j / 2), lane);
+  __builtin_amdgcn_sched_barrier(0);
   // the causal mask only bites on the half-tiles that reach past the wave's first query
   if (kh + 31 > qw0) {
 #pragma unroll
@@ -60,12 +79,15 @@ __device__ __forceinline__ void fwd_half(const T* ks, const T* vs, int r0, int k
   }
   // O^T += V^T P^T over the 32 keys, contraction in the permuted key order of pb (element e of
   // chunk c2 is key kh + 16 c2 + 8 (e / 4) + 4 hi + e % 4); V^T read transposed out of the
-  // row-major V tile.
+  // row-major V tile, two operands ahead of the MFMAs
+  __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-  for (int md = 0; md < D / 32; ++md)
-#pragma unroll
-    for (int c2 = 0; c2 < 2; ++c2)
-      oacc[md] = Mfma<T>::run(ld_tr<V8, KP>(vs, r0 + 16 * c2, 32 * md, lane), pb[c2], oacc[md]);
+  for (int j = 0; j < 2 * (D / 32); ++j) {
+    oacc[j / 2] = Mfma<T>::run(vbuf[j % VA], pb[j % 2], oacc[j / 2]);
+    if (j + VA < 2 * (D / 32))
+      vbuf[j % VA] = ld_tr<V8, KP>(vs, r0 + 16 * ((j + VA) % 2), 32 * ((j + VA) / 2), lane);
+    __builtin_amdgcn_sched_barrier(0);
+  }
 }
 
 // The D = 64 forward: K / V staged through registers in 64-key tiles (rows of 128 bytes).
