@@ -89,13 +89,20 @@ __device__ __forceinline__ int64_t token_pos(const RopeArgs& a, int64_t b, int64
   return s;
 }
 
-// The TPW tokens of one wavefront. Heads go in groups of PG passes per token (TPW * PG = 4
-// passes in total); each group issues every load of every token before any rotation.
+// The raw (still packed) halves of one group of heads of the TPW tokens of a wavefront: heads
+// go in groups of PG passes per token (TPW * PG = 4 passes in total).
+template <typename T, int TPW, int PG>
+struct RopeGroup {
+  Raw<T> x1[TPW][PG], x2[TPW][PG], d1[TPW][PG], d2[TPW][PG];
+};
+
+// Issue every load of the head group starting at head h0 (all tokens, all passes) before any
+// is used.
 template <bool VEC, bool QD, typename T, int HALF, int TPW>
-__device__ __forceinline__ void rope_tokens(const RopeArgs& a, const int64_t (&bb)[TPW],
-                                            const int64_t (&ss)[TPW], const bool (&live)[TPW],
-                                            int lane, const float (&cv)[TPW][8],
-                                            const float (&sv)[TPW][8]) {
+__device__ __forceinline__ void rope_load(const RopeArgs& a, const int64_t (&bb)[TPW],
+                                          const int64_t (&ss)[TPW], const bool (&live)[TPW],
+                                          int lane, int h0,
+                                          RopeGroup<T, TPW, kRopePasses / TPW>& g) {
   constexpr int LPH = HALF / 8;
   constexpr int HPP = kWave / LPH;
   constexpr int PG = kRopePasses / TPW;
@@ -105,62 +112,73 @@ __device__ __forceinline__ void rope_tokens(const RopeArgs& a, const int64_t (&b
   const T* __restrict__ q = static_cast<const T*>(a.q);
   const T* __restrict__ qd = static_cast<const T*>(a.qd);
   const T* __restrict__ k = static_cast<const T*>(a.k);
-  T* __restrict__ qo = static_cast<T*>(a.qo);
-  T* __restrict__ ko = static_cast<T*>(a.ko);
-
-  for (int h0 = 0; h0 < nh; h0 += PG * HPP) {
-    Raw<T> x1[TPW][PG], x2[TPW][PG], d1[TPW][PG], d2[TPW][PG];
 #pragma unroll
-    for (int t = 0; t < TPW; ++t) {
+  for (int t = 0; t < TPW; ++t) {
 #pragma unroll
-      for (int i = 0; i < PG; ++i) {
-        const int h = h0 + i * HPP + hs;
-        if (live[t] && h < nh) {
-          const T* src = h < a.HQ
-              ? q + bb[t] * a.q_s[0] + ss[t] * a.q_s[1] + (int64_t)h * a.q_s[2]
-              : k + bb[t] * a.k_s[0] + ss[t] * a.k_s[1] + (int64_t)(h - a.HQ) * a.k_s[2];
-          x1[t][i] = ld_raw<VEC>(src + 8 * c);
-          x2[t][i] = ld_raw<VEC>(src + HALF + 8 * c);
-          if (QD && h < a.HQ) {
-            const T* dsrc = qd + bb[t] * a.qd_s[0] + ss[t] * a.qd_s[1] + (int64_t)h * a.qd_s[2];
-            d1[t][i] = ld_raw<VEC>(dsrc + 8 * c);
-            d2[t][i] = ld_raw<VEC>(dsrc + HALF + 8 * c);
-          }
+    for (int i = 0; i < PG; ++i) {
+      const int h = h0 + i * HPP + hs;
+      if (live[t] && h < nh) {
+        const T* src = h < a.HQ
+            ? q + bb[t] * a.q_s[0] + ss[t] * a.q_s[1] + (int64_t)h * a.q_s[2]
+            : k + bb[t] * a.k_s[0] + ss[t] * a.k_s[1] + (int64_t)(h - a.HQ) * a.k_s[2];
+        g.x1[t][i] = ld_raw<VEC>(src + 8 * c);
+        g.x2[t][i] = ld_raw<VEC>(src + HALF + 8 * c);
+        if (QD && h < a.HQ) {
+          const T* dsrc = qd + bb[t] * a.qd_s[0] + ss[t] * a.qd_s[1] + (int64_t)h * a.qd_s[2];
+          g.d1[t][i] = ld_raw<VEC>(dsrc + 8 * c);
+          g.d2[t][i] = ld_raw<VEC>(dsrc + HALF + 8 * c);
         }
       }
     }
+  }
+}
+
+// Rotate and store the head group starting at h0.
+template <bool VEC, bool QD, typename T, int HALF, int TPW>
+__device__ __forceinline__ void rope_store(const RopeArgs& a, const int64_t (&bb)[TPW],
+                                           const int64_t (&ss)[TPW], const bool (&live)[TPW],
+                                           int lane, int h0,
+                                           const RopeGroup<T, TPW, kRopePasses / TPW>& g,
+                                           const float (&cv)[TPW][8], const float (&sv)[TPW][8]) {
+  constexpr int LPH = HALF / 8;
+  constexpr int HPP = kWave / LPH;
+  constexpr int PG = kRopePasses / TPW;
+  const int c = lane % LPH;
+  const int hs = lane / LPH;
+  const int nh = a.HQ + a.HK;
+  T* __restrict__ qo = static_cast<T*>(a.qo);
+  T* __restrict__ ko = static_cast<T*>(a.ko);
 #pragma unroll
-    for (int t = 0; t < TPW; ++t) {
+  for (int t = 0; t < TPW; ++t) {
 #pragma unroll
-      for (int i = 0; i < PG; ++i) {
-        const int h = h0 + i * HPP + hs;
-        if (live[t] && h < nh) {
-          float u1[8], u2[8];
-          Buf<T>::unpack(x1[t][i], u1);
-          Buf<T>::unpack(x2[t][i], u2);
-          if (QD && h < a.HQ) {
-            // q + q_delta in the storage dtype (one rounding), as the unfused model adds them
-            float e1[8], e2[8];
-            Buf<T>::unpack(d1[t][i], e1);
-            Buf<T>::unpack(d2[t][i], e2);
-#pragma unroll
-            for (int e = 0; e < 8; ++e) {
-              u1[e] = Elt<T>::round(u1[e] + e1[e]);
-              u2[e] = Elt<T>::round(u2[e] + e2[e]);
-            }
-          }
-          float o1[8], o2[8];
+    for (int i = 0; i < PG; ++i) {
+      const int h = h0 + i * HPP + hs;
+      if (live[t] && h < nh) {
+        float u1[8], u2[8];
+        Buf<T>::unpack(g.x1[t][i], u1);
+        Buf<T>::unpack(g.x2[t][i], u2);
+        if (QD && h < a.HQ) {
+          // q + q_delta in the storage dtype (one rounding), as the unfused model adds them
+          float e1[8], e2[8];
+          Buf<T>::unpack(g.d1[t][i], e1);
+          Buf<T>::unpack(g.d2[t][i], e2);
 #pragma unroll
           for (int e = 0; e < 8; ++e) {
-            o1[e] = u1[e] * cv[t][e] - u2[e] * sv[t][e];
-            o2[e] = u2[e] * cv[t][e] + u1[e] * sv[t][e];
+            u1[e] = Elt<T>::round(u1[e] + e1[e]);
+            u2[e] = Elt<T>::round(u2[e] + e2[e]);
           }
-          T* dst = h < a.HQ
-              ? qo + bb[t] * a.qo_s[0] + ss[t] * a.qo_s[1] + (int64_t)h * a.qo_s[2]
-              : ko + bb[t] * a.ko_s[0] + ss[t] * a.ko_s[1] + (int64_t)(h - a.HQ) * a.ko_s[2];
-          st_half<VEC>(dst + 8 * c, o1);
-          st_half<VEC>(dst + HALF + 8 * c, o2);
         }
+        float o1[8], o2[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          o1[e] = u1[e] * cv[t][e] - u2[e] * sv[t][e];
+          o2[e] = u2[e] * cv[t][e] + u1[e] * sv[t][e];
+        }
+        T* dst = h < a.HQ
+            ? qo + bb[t] * a.qo_s[0] + ss[t] * a.qo_s[1] + (int64_t)h * a.qo_s[2]
+            : ko + bb[t] * a.ko_s[0] + ss[t] * a.ko_s[1] + (int64_t)(h - a.HQ) * a.ko_s[2];
+        st_half<VEC>(dst + 8 * c, o1);
+        st_half<VEC>(dst + HALF + 8 * c, o2);
       }
     }
   }
@@ -182,6 +200,19 @@ __global__ __launch_bounds__(kRopeWaves * kWave) void k_rope(const RopeArgs a) {
     const int64_t tt = live[t] ? t0 + t : t0;
     bb[t] = tt / a.S;
     ss[t] = tt - bb[t] * a.S;
+  }
+  // With two tokens per wavefront (few heads: the launch is short and latency-bound) the first
+  // head group's loads go out before the angles are worked out (an inv_freq and position read,
+  // sincosf, the LDS round), which then overlap the data's memory round trip: config 4
+  // 11.6 -> 10.6 us per launch. With one token per wavefront (many heads, a long launch at the
+  // bandwidth limit) the loads follow the angles: issued first they made config 5 5% slower.
+  constexpr int PG = kRopePasses / TPW;
+  constexpr int HPP = kWave / (HALF / 8);
+  constexpr bool kLoadFirst = TPW == 2;
+  RopeGroup<T, TPW, PG> g;
+  if constexpr (kLoadFirst) rope_load<VEC, QD, T, HALF, TPW>(a, bb, ss, live, lane, 0, g);
+#pragma unroll
+  for (int t = 0; t < TPW; ++t) {
     const float p = (float)token_pos(a, bb[t], ss[t], lane);
     for (int j = lane; j < HALF; j += kWave) {
       const float ang = p * a.inv_freq[j];
@@ -206,7 +237,12 @@ __global__ __launch_bounds__(kRopeWaves * kWave) void k_rope(const RopeArgs a) {
     sv[t][0] = s0.x; sv[t][1] = s0.y; sv[t][2] = s0.z; sv[t][3] = s0.w;
     sv[t][4] = s1.x; sv[t][5] = s1.y; sv[t][6] = s1.z; sv[t][7] = s1.w;
   }
-  rope_tokens<VEC, QD, T, HALF, TPW>(a, bb, ss, live, lane, cv, sv);
+  if constexpr (!kLoadFirst) rope_load<VEC, QD, T, HALF, TPW>(a, bb, ss, live, lane, 0, g);
+  rope_store<VEC, QD, T, HALF, TPW>(a, bb, ss, live, lane, 0, g, cv, sv);
+  for (int h0 = PG * HPP; h0 < a.HQ + a.HK; h0 += PG * HPP) {
+    rope_load<VEC, QD, T, HALF, TPW>(a, bb, ss, live, lane, h0, g);
+    rope_store<VEC, QD, T, HALF, TPW>(a, bb, ss, live, lane, h0, g, cv, sv);
+  }
 }
 
 // Tokens per wavefront: two when a token's heads fit in at most two passes (each lane then
