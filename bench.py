@@ -295,13 +295,14 @@ def time_graph(g, reps):
     return e0.elapsed_time(e1) / reps, (t1 - t0) * 1e3 / reps
 
 
-def api_bytes(T, H, k_dy, fwd):
+def api_bytes(T, H, k_dy, fwd, x_bytes=4):
     """The reference API's pattern (AddRMSNorm in the packed decoder): fp32 residual r, bf16
-    delta / y / dys, fp32 r_out / dr_out / dr, bf16 ddelta, rstd saved, frozen weight (no dw)."""
+    delta / y / dys, fp32 r_out / dr_out / dr, bf16 ddelta, rstd saved, frozen weight (no dw).
+    x_bytes: the backward's xhat source, the fp32 r_out (4) or, in save-output mode, y (2)."""
     if fwd:  # r_in, delta -> r_out, y, rstd
         return T * H * (4 + 2 + 4 + 2) + 4 * T
-    # k dys, x (= r_out), dr_out -> dr, ddelta; rstd read
-    return T * H * (2 * k_dy + 4 + 4 + 4 + 2) + 4 * T
+    # k dys, x (r_out or y), dr_out -> dr, ddelta; rstd read
+    return T * H * (2 * k_dy + x_bytes + 4 + 4 + 2) + 4 * T
 
 
 def run_api_variant(dev, reps, n_sets=6):
@@ -335,6 +336,12 @@ def run_api_variant(dev, reps, n_sets=6):
         "add_rmsnorm_bwd_2dy": (lambda: [_hip.rmsnorm_bwd(s["dys"][:2], s["r"], s["w"], eps, rstd=s["rstd"],
                                                           dr_out=s["dro"], dr=s["dr"], dx=s["dd"]) for s in sets],
                                 api_bytes(T, H, 2, False)),
+        # the reference decoder's default (NORM_SAVE_OUTPUT): xhat recovered from the saved y
+        # (y / w; a weight of 1 + 0.02 N(0, 1) has no exact channels)
+        "add_rmsnorm_bwd_3dy_from_y": (lambda: [_hip.rmsnorm_bwd(s["dys"], s["y"], s["w"], eps, from_y=True,
+                                                                 rstd=s["rstd"], dr_out=s["dro"], dr=s["dr"],
+                                                                 dx=s["dd"]) for s in sets],
+                                       api_bytes(T, H, 3, False, x_bytes=2)),
     }
     out = {}
     for name, (fn, nbytes) in calls.items():
@@ -348,7 +355,8 @@ def run_api_variant(dev, reps, n_sets=6):
     torch.cuda.empty_cache()
     return {"workload": "the reference API's calls at T=8192, H=1536: add_rmsnorm forward (fp32 r_in + "
                         "bf16 delta -> fp32 r_out, bf16 y, rstd) and AddRMSNorm backward with 3 or 2 "
-                        "bf16 dys and fp32 dr_out -> fp32 dr + bf16 ddelta (frozen weight, rstd saved)",
+                        "bf16 dys and fp32 dr_out -> fp32 dr + bf16 ddelta (frozen weight, rstd saved)"
+                        "; the 3-dy backward also in save-output mode (xhat from the bf16 y)",
             "kernels": out}
 
 

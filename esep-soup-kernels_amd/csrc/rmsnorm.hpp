@@ -301,15 +301,19 @@ __device__ __forceinline__ void bwd_rows(const BwdArgs& a, float* red, float* ld
 
       // x -> xhat
       if (a.from_y) {
-        // xhat = y / w for the columns of the row (0 beyond it: no 0 / 0); the exact
-        // channels come from xs.
+        // xhat = y / w for the columns of the row (0 beyond it: no 0 / 0), as y times the
+        // hardware reciprocal of w (v_rcp_f32, about 1 ulp; the reference's Triton division
+        // is itself approximate, and y carries 16-bit rounding): the correctly rounded
+        // division costs ~10 instructions per element and made this call compute-bound. The
+        // exact channels (w tiny, huge or not finite) come from xs.
 #pragma unroll
         for (int k = 0; k < NV; ++k) {
           const int col = 8 * (tg + k * G);
           float w8[8];
           bload<VEC, float, kCached>(rw, col * 4, w8);
 #pragma unroll
-          for (int e = 0; e < 8; ++e) x[k][e] = x[k][e] / (col + e < n ? w8[e] : 1.f);
+          for (int e = 0; e < 8; ++e)
+            x[k][e] = x[k][e] * __builtin_amdgcn_rcpf(col + e < n ? w8[e] : 1.f);
         }
         if (a.n_special > 0 && ok) {
           const Span rs = make_span(a.slot, (uint32_t)n * 4u);
