@@ -186,6 +186,56 @@ __device__ __forceinline__ void fwd_rows(const FwdArgs& a, float* red) {
   }
 }
 
+// The plain forward (no delta, no exact channels) with one wavefront per row (n <= 1536) and RPW
+// rows per wavefront: every row's x is loaded (raw, still packed) before any row is reduced.
+template <int NV, typename TX, typename TY, int RPW>
+__device__ __forceinline__ void fwd_rows_multi(const FwdArgs& a) {
+  const int gpb = a.gpb;
+  const int grp = wave_id();
+  const int tg = (int)threadIdx.x - grp * kWave;
+  const int n = a.n;
+  const int64_t row0 = ((int64_t)blockIdx.x * gpb + grp) * RPW;
+  Raw<TX> rx[RPW][NV];
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const int64_t row = row0 + r;
+    const Span sx = row_rsrc<TX>(a.x, row, a.ld_x, n, row < a.rows);
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+      rx[r][k] = Buf<TX>::template load_raw<kStream>(sx, (tg + k * kWave) * 8 * sizeof(TX));
+  }
+  const Span rw = make_span(a.w, (uint32_t)n * 4u);
+#pragma unroll
+  for (int r = 0; r < RPW; ++r) {
+    const int64_t row = row0 + r;
+    const bool ok = row < a.rows;
+    float v[NV][8];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) Buf<TX>::unpack(rx[r][k], v[k]);
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(v[k][e], v[k][e], ss);
+    const float inv = inv_rms(wave_sum(ss), n, a.eps);
+    const Span ry = row_rsrc<TY>(a.y, row, a.ld_y, n, ok);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      float w8[8], o[8];
+      bload<true, float, kCached>(rw, (tg + k * kWave) * 32, w8);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[e] = w8[e] * (v[k][e] * inv);
+      bstore<true, TY>(ry, (tg + k * kWave) * 8 * sizeof(TY), o);
+    }
+    if (a.rstd != nullptr && ok && tg == 0) a.rstd[row] = inv;
+  }
+}
+
+template <int NV, typename TX, typename TY, int RPW>
+__global__ __launch_bounds__(256) void k_rmsnorm_fwd_multi(const FwdArgs a) {
+  fwd_rows_multi<NV, TX, TY, RPW>(a);
+}
+
 // VEC kernels are instantiated for NV = 2, 3; the element-wise (!VEC) kernel only for
 // NV = 3, which serves every row width (surplus chunks lie past the row and read 0).
 template <int NV, bool VEC, typename TX, typename TD, typename TY>

@@ -7,8 +7,22 @@
 
 namespace esep {
 
+// Rows per wavefront of the plain forward at n <= 1536 (one wavefront per row). Measured at
+// config 4 (8192 x 1536 bf16, per launch): 1 row 9.97 us, 2 10.2, 3 10.06, 4 9.79, 6 12.96,
+// 8 12.04 (too few wavefronts left).
+constexpr int kFwdRowsPerWave = 4;
+
 template <typename TX, typename TD, typename TY>
 static hipError_t fwd_nv(const FwdArgs& a, int nv, dim3 grid, dim3 block, hipStream_t s) {
+  if constexpr (std::is_void_v<TD>) {
+    if (a.vec && a.wpr == 1 && a.n_special == 0 && block.x == 256) {
+      constexpr int RPW = kFwdRowsPerWave;
+      const dim3 g((unsigned)((a.rows + 4 * RPW - 1) / (4 * RPW)));
+      if (nv == 2) hipLaunchKernelGGL((k_rmsnorm_fwd_multi<2, TX, TY, RPW>), g, block, 0, s, a);
+      else hipLaunchKernelGGL((k_rmsnorm_fwd_multi<3, TX, TY, RPW>), g, block, 0, s, a);
+      return hipGetLastError();
+    }
+  }
   if (!a.vec) {
     hipLaunchKernelGGL((k_rmsnorm_fwd<3, false, TX, TD, TY>), grid, block, 0, s, a);
     return hipGetLastError();
