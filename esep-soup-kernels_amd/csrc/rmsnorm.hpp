@@ -186,13 +186,14 @@ __device__ __forceinline__ void fwd_rows(const FwdArgs& a, float* red) {
   }
 }
 
-// The plain forward (no delta, no exact channels) with one wavefront per row (n <= 1536) and RPW
-// rows per wavefront: every row's x is loaded (raw, still packed) before any row is reduced.
+// The plain forward (no delta, no exact channels) with RPW rows per row group: every row's x
+// is loaded (raw, still packed) before any row is reduced.
 template <int NV, typename TX, typename TY, int RPW>
-__device__ __forceinline__ void fwd_rows_multi(const FwdArgs& a) {
+__device__ __forceinline__ void fwd_rows_multi(const FwdArgs& a, float* red) {
+  const int G = kWave * a.wpr;
   const int gpb = a.gpb;
-  const int grp = wave_id();
-  const int tg = (int)threadIdx.x - grp * kWave;
+  const int grp = wave_id() / a.wpr;
+  const int tg = (int)threadIdx.x - grp * G;
   const int n = a.n;
   const int64_t row0 = ((int64_t)blockIdx.x * gpb + grp) * RPW;
   Raw<TX> rx[RPW][NV];
@@ -202,7 +203,7 @@ __device__ __forceinline__ void fwd_rows_multi(const FwdArgs& a) {
     const Span sx = row_rsrc<TX>(a.x, row, a.ld_x, n, row < a.rows);
 #pragma unroll
     for (int k = 0; k < NV; ++k)
-      rx[r][k] = Buf<TX>::template load_raw<kStream>(sx, (tg + k * kWave) * 8 * sizeof(TX));
+      rx[r][k] = Buf<TX>::template load_raw<kStream>(sx, (tg + k * G) * 8 * sizeof(TX));
   }
   const Span rw = make_span(a.w, (uint32_t)n * 4u);
 #pragma unroll
@@ -217,23 +218,24 @@ __device__ __forceinline__ void fwd_rows_multi(const FwdArgs& a) {
     for (int k = 0; k < NV; ++k)
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss = fmaf(v[k][e], v[k][e], ss);
-    const float inv = inv_rms(wave_sum(ss), n, a.eps);
+    const float inv = inv_rms(row_sum(ss, a.wpr, red), n, a.eps);
     const Span ry = row_rsrc<TY>(a.y, row, a.ld_y, n, ok);
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
       float w8[8], o[8];
-      bload<true, float, kCached>(rw, (tg + k * kWave) * 32, w8);
+      bload<true, float, kCached>(rw, (tg + k * G) * 32, w8);
 #pragma unroll
       for (int e = 0; e < 8; ++e) o[e] = w8[e] * (v[k][e] * inv);
-      bstore<true, TY>(ry, (tg + k * kWave) * 8 * sizeof(TY), o);
+      bstore<true, TY>(ry, (tg + k * G) * 8 * sizeof(TY), o);
     }
     if (a.rstd != nullptr && ok && tg == 0) a.rstd[row] = inv;
   }
 }
 
 template <int NV, typename TX, typename TY, int RPW>
-__global__ __launch_bounds__(256) void k_rmsnorm_fwd_multi(const FwdArgs a) {
-  fwd_rows_multi<NV, TX, TY, RPW>(a);
+__global__ __launch_bounds__(kFwdMaxThreads) void k_rmsnorm_fwd_multi(const FwdArgs a) {
+  __shared__ float red[kFwdMaxThreads / kWave];
+  fwd_rows_multi<NV, TX, TY, RPW>(a, red);
 }
 
 // VEC kernels are instantiated for NV = 2, 3; the element-wise (!VEC) kernel only for

@@ -9,7 +9,9 @@ namespace esep {
 
 // Rows per wavefront of the plain forward at n <= 1536 (one wavefront per row). Measured at
 // config 4 (8192 x 1536 bf16, per launch): 1 row 9.97 us, 2 10.2, 3 10.06, 4 9.79, 6 12.96,
-// 8 12.04 (too few wavefronts left).
+// 8 12.04 (too few wavefronts left); 4 rows built under the 1024-thread bound (78 VGPRs, the
+// compiler schedules the loads differently) 9.05. Rows per group with several wavefronts per
+// row (n > 1536) measured slower at config 5 (2 to 4 rows: 174-175 us against 170).
 constexpr int kFwdRowsPerWave = 4;
 
 template <typename TX, typename TD, typename TY>
