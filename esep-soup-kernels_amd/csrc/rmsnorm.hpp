@@ -186,9 +186,9 @@ __device__ __forceinline__ void fwd_rows(const FwdArgs& a, float* red) {
   }
 }
 
-// The plain forward (no delta, no exact channels) with RPW rows per row group: every row's x
-// is loaded (raw, still packed) before any row is reduced.
-template <int NV, typename TX, typename TY, int RPW>
+// The forward without exact channels (plain, or residual add with a delta) with RPW rows per
+// row group: every row's x (and delta) is loaded (raw, still packed) before any row is reduced.
+template <int NV, typename TX, typename TD, typename TY, int RPW>
 __device__ __forceinline__ void fwd_rows_multi(const FwdArgs& a, float* red) {
   const int G = kWave * a.wpr;
   const int gpb = a.gpb;
@@ -196,7 +196,10 @@ __device__ __forceinline__ void fwd_rows_multi(const FwdArgs& a, float* red) {
   const int tg = (int)threadIdx.x - grp * G;
   const int n = a.n;
   const int64_t row0 = ((int64_t)blockIdx.x * gpb + grp) * RPW;
+  constexpr bool kDelta = !std::is_void_v<TD>;
+  using TDR = std::conditional_t<kDelta, TD, TX>;  // a type for the unused delta registers
   Raw<TX> rx[RPW][NV];
+  Raw<TDR> rd[kDelta ? RPW : 1][NV];
 #pragma unroll
   for (int r = 0; r < RPW; ++r) {
     const int64_t row = row0 + r;
@@ -204,6 +207,12 @@ __device__ __forceinline__ void fwd_rows_multi(const FwdArgs& a, float* red) {
 #pragma unroll
     for (int k = 0; k < NV; ++k)
       rx[r][k] = Buf<TX>::template load_raw<kStream>(sx, (tg + k * G) * 8 * sizeof(TX));
+    if constexpr (kDelta) {
+      const Span sd = row_rsrc<TD>(a.delta, row, a.ld_d, n, row < a.rows);
+#pragma unroll
+      for (int k = 0; k < NV; ++k)
+        rd[r][k] = Buf<TD>::template load_raw<kStream>(sd, (tg + k * G) * 8 * sizeof(TD));
+    }
   }
   const Span rw = make_span(a.w, (uint32_t)n * 4u);
 #pragma unroll
@@ -213,6 +222,20 @@ __device__ __forceinline__ void fwd_rows_multi(const FwdArgs& a, float* red) {
     float v[NV][8];
 #pragma unroll
     for (int k = 0; k < NV; ++k) Buf<TX>::unpack(rx[r][k], v[k]);
+    if constexpr (kDelta) {
+#pragma unroll
+      for (int k = 0; k < NV; ++k) {
+        float d[8];
+        Buf<TD>::unpack(rd[r][k], d);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[k][e] = Elt<TX>::round(v[k][e] + d[e]);
+      }
+      if (a.r_out != nullptr) {
+        const Span rr = row_rsrc<TX>(a.r_out, row, a.ld_r, n, ok);
+#pragma unroll
+        for (int k = 0; k < NV; ++k) bstore<true, TX>(rr, (tg + k * G) * 8 * sizeof(TX), v[k]);
+      }
+    }
     float ss = 0.f;
 #pragma unroll
     for (int k = 0; k < NV; ++k)
@@ -232,10 +255,10 @@ __device__ __forceinline__ void fwd_rows_multi(const FwdArgs& a, float* red) {
   }
 }
 
-template <int NV, typename TX, typename TY, int RPW>
+template <int NV, typename TX, typename TD, typename TY, int RPW>
 __global__ __launch_bounds__(kFwdMaxThreads) void k_rmsnorm_fwd_multi(const FwdArgs a) {
   __shared__ float red[kFwdMaxThreads / kWave];
-  fwd_rows_multi<NV, TX, TY, RPW>(a, red);
+  fwd_rows_multi<NV, TX, TD, TY, RPW>(a, red);
 }
 
 // VEC kernels are instantiated for NV = 2, 3; the element-wise (!VEC) kernel only for

@@ -13,15 +13,18 @@ namespace esep {
 // compiler schedules the loads differently) 9.05. Rows per group with several wavefronts per
 // row (n > 1536) measured slower at config 5 (2 to 4 rows: 174-175 us against 170).
 constexpr int kFwdRowsPerWave = 4;
+// With a delta (the reference API's add_rmsnorm: fp32 residual + bf16 delta -> fp32 r_out, bf16
+// y at 8192 x 1536): 1 row 31.3 us against 32.0 for the general kernel, 2 rows 31.6, 4 rows 37.7.
+constexpr int kFwdDeltaRowsPerWave = 1;
 
 template <typename TX, typename TD, typename TY>
 static hipError_t fwd_nv(const FwdArgs& a, int nv, dim3 grid, dim3 block, hipStream_t s) {
-  if constexpr (std::is_void_v<TD>) {
+  constexpr int RPW = std::is_void_v<TD> ? kFwdRowsPerWave : kFwdDeltaRowsPerWave;
+  if constexpr (RPW > 0) {
     if (a.vec && a.wpr == 1 && a.n_special == 0 && block.x == 256) {
-      constexpr int RPW = kFwdRowsPerWave;
       const dim3 g((unsigned)((a.rows + 4 * RPW - 1) / (4 * RPW)));
-      if (nv == 2) hipLaunchKernelGGL((k_rmsnorm_fwd_multi<2, TX, TY, RPW>), g, block, 0, s, a);
-      else hipLaunchKernelGGL((k_rmsnorm_fwd_multi<3, TX, TY, RPW>), g, block, 0, s, a);
+      if (nv == 2) hipLaunchKernelGGL((k_rmsnorm_fwd_multi<2, TX, TD, TY, RPW>), g, block, 0, s, a);
+      else hipLaunchKernelGGL((k_rmsnorm_fwd_multi<3, TX, TD, TY, RPW>), g, block, 0, s, a);
       return hipGetLastError();
     }
   }
