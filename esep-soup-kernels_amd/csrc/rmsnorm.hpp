@@ -583,6 +583,104 @@ __device__ __forceinline__ void bwd_rows_fast(const BwdArgs& a, float* red, floa
   }
 }
 
+// Backward of the reference API's calls without a weight gradient or exact channels (up to 5
+// gradients of y, dr_out, xhat from x or from y = w * xhat) in blocks of at most 256 threads:
+// every load of a row (all dys, x, dr_out) is issued before any is used. The general kernel
+// keeps within 128 registers by loading them one after another, a chain of dependent memory
+// round trips per row. Inputs that are absent get 0-byte buffers: they read 0 and cost no
+// memory access, and the absent gradients add +0 (the same sums as the general kernel).
+constexpr int kBwdApiThreads = 256;
+template <int NV, typename TX, typename TDY, typename TO>
+__global__ __launch_bounds__(kBwdApiThreads) void k_rmsnorm_bwd_api(const BwdArgs a) {
+  __shared__ float red[kBwdApiThreads / kWave];
+  const int G = kWave * a.wpr;
+  const int grp = wave_id() / a.wpr;
+  const int tg = (int)threadIdx.x - grp * G;
+  const int n = a.n;
+  const int64_t row = (int64_t)blockIdx.x * a.gpb + grp;
+  const bool ok = row < a.rows;
+  Raw<TDY> rdy[kMaxDy][NV];
+  Raw<TX> rx[NV];
+  Raw<float> ro[NV];
+#pragma unroll
+  for (int i = 0; i < kMaxDy; ++i) {
+    const Span sd = row_rsrc<TDY>(a.dy[i], row, a.ld_dy, n, ok && i < a.n_dy);
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+      rdy[i][k] = Buf<TDY>::template load_raw<kStream>(sd, (tg + k * G) * 8 * sizeof(TDY));
+  }
+  {
+    const Span sx = row_rsrc<TX>(a.x, row, a.ld_x, n, ok);
+    const Span so = row_rsrc<float>(a.dr_out, row, a.ld_out, n, ok && a.dr_out != nullptr);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      rx[k] = Buf<TX>::template load_raw<kStream>(sx, (tg + k * G) * 8 * sizeof(TX));
+      ro[k] = Buf<float>::template load_raw<kStream>(so, (tg + k * G) * 32);
+    }
+  }
+  const float rstd_saved = (a.rstd != nullptr && ok) ? a.rstd[row] : 1.f;
+  const Span rw = make_span(a.w, (uint32_t)n * 4u);
+
+  float dy[NV][8], x[NV][8];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    Buf<TDY>::unpack(rdy[0][k], dy[k]);
+    Buf<TX>::unpack(rx[k], x[k]);
+  }
+#pragma unroll
+  for (int i = 1; i < kMaxDy; ++i)
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      float t[8];
+      Buf<TDY>::unpack(rdy[i][k], t);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dy[k][e] += t[e];
+    }
+  float inv = rstd_saved;
+  if (a.rstd == nullptr) {  // recomputed from x (from_y always has the saved rstd)
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(x[k][e], x[k][e], ss);
+    inv = inv_rms(row_sum(ss, a.wpr, red), n, a.eps);
+  }
+  float p = 0.f;
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    float w8[8];
+    bload<true, float, kCached>(rw, (tg + k * G) * 32, w8);
+    const int col = 8 * (tg + k * G);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      // xhat = x * rstd, or y times the hardware reciprocal of w (as the general kernel)
+      x[k][e] = a.from_y ? x[k][e] * __builtin_amdgcn_rcpf(col + e < n ? w8[e] : 1.f)
+                         : x[k][e] * inv;
+      dy[k][e] *= w8[e];
+      p = fmaf(dy[k][e], x[k][e], p);
+    }
+  }
+  const float proj = row_sum(p, a.wpr, red) / (float)n;
+  float dr[NV][8];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) {
+    float t[8];
+    Buf<float>::unpack(ro[k], t);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dr[k][e] = inv * (dy[k][e] - x[k][e] * proj) + t[e];
+  }
+  if (a.dr != nullptr) {
+    const Span so = row_rsrc<float>(a.dr, row, a.ld_out, n, ok);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) bstore<true, float>(so, (tg + k * G) * 32, dr[k]);
+  }
+  if (a.dx != nullptr) {
+    const Span so = row_rsrc<TO>(a.dx, row, a.ld_out, n, ok);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) bstore<true, TO>(so, (tg + k * G) * 8 * sizeof(TO), dr[k]);
+  }
+}
+
 // FAST: bwd_rows_fast (only with VEC); else the general bwd_rows.
 template <int NV, bool VEC, bool FAST, typename TX, typename TDY, typename TO>
 __global__ __launch_bounds__(kBwdThreads) void k_rmsnorm_bwd(const BwdArgs a) {

@@ -17,6 +17,13 @@ static hipError_t bwd_nv(const BwdArgs& a, int nv, dim3 grid, dim3 block, size_t
   }
   // The fast kernel serves the plain backward: one dy, xhat from x, no dr_out.
   const bool fast = a.n_dy == 1 && !a.from_y && a.dr_out == nullptr && a.n_special == 0;
+  // The reference API's other calls without a weight gradient or exact channels.
+  if (!fast && a.part == nullptr && a.n_special == 0 && a.n_dy > 0 &&
+      block.x <= (unsigned)kBwdApiThreads) {
+    if (nv == 2) hipLaunchKernelGGL((k_rmsnorm_bwd_api<2, TX, TDY, TO>), grid, block, 0, s, a);
+    else hipLaunchKernelGGL((k_rmsnorm_bwd_api<3, TX, TDY, TO>), grid, block, 0, s, a);
+    return hipGetLastError();
+  }
   switch (nv * 2 + (fast ? 1 : 0)) {
     case 4: hipLaunchKernelGGL((k_rmsnorm_bwd<2, true, false, TX, TDY, TO>), grid, block, lds, s, a); break;
     case 5: hipLaunchKernelGGL((k_rmsnorm_bwd<2, true, true, TX, TDY, TO>), grid, block, lds, s, a); break;
