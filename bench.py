@@ -624,6 +624,78 @@ def run_lm_head(dev, reps):
                         f"{rows}-row chunk", "gemm_flops": int(flops), **out}
 
 
+def run_packed_decoder(dev, reps, layers=28):
+    """The reference's patch point end to end (solution/body/packed.py): a Qwen2.5-1.5B-shaped
+    Qwen2Model (random weights on the device, `layers` decoder layers, hidden 1536, 12 / 2
+    heads, MLP 8960) in the reference's training setup (fp32 master weights, bf16 autocast; base
+    frozen except q_proj / v_proj, as a LoRA run freezes it), forward + backward on 8 rows padded
+    to 1024 tokens with lengths U[512, 1024] (seed 0): the patched forward (pad removal, HIP
+    norms, RoPE, varlen attention, SwiGLU recompute MLP) against HF's original forward (sdpa)
+    on the same GPU and inputs."""
+    import torch
+    from transformers import Qwen2Config, Qwen2Model
+    from transformers.models.qwen2 import modeling_qwen2
+
+    from solution import body
+    from solution.body import _hip
+
+    body.patch()
+    cfg = Qwen2Config(vocab_size=151936, hidden_size=1536, intermediate_size=8960,
+                      num_hidden_layers=layers, num_attention_heads=12, num_key_value_heads=2,
+                      head_dim=128, max_position_embeddings=32768, rms_norm_eps=1e-6,
+                      rope_theta=1e6, use_cache=False, tie_word_embeddings=True)
+    cfg._attn_implementation = "sdpa"
+    torch.manual_seed(0)
+    with torch.device(dev):
+        model = Qwen2Model(cfg)
+    for name, p in model.named_parameters():
+        p.requires_grad_(name.endswith(("q_proj.weight", "v_proj.weight")))
+    model.train()
+    g = torch.Generator().manual_seed(0)
+    lens = torch.randint(512, 1025, (8,), generator=g)
+    ids = torch.randint(0, cfg.vocab_size, (8, 1024), generator=g).to(dev)
+    mask = (torch.arange(1024)[None, :] < lens[:, None]).long().to(dev)
+
+    def step():
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            out = model(input_ids=ids, attention_mask=mask).last_hidden_state
+        out.float().square().mean().backward()
+
+    def timed():
+        for _ in range(2):
+            step()
+        torch.cuda.synchronize()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            step()
+        e1.record()
+        torch.cuda.synchronize()
+        return e0.elapsed_time(e1) / reps
+
+    with _hip.count_launches() as names:
+        step()
+        torch.cuda.synchronize()
+    ours = timed()
+    cls = modeling_qwen2.Qwen2Model
+    patched = cls.forward
+    cls.forward = patched.__wrapped__
+    try:
+        hf = timed()
+    finally:
+        cls.forward = patched
+    log(f"packed decoder ({layers} layers): {ours:.2f} ms vs HF's original forward {hf:.2f} ms")
+    del model
+    torch.cuda.empty_cache()
+    return {"workload": f"Qwen2.5-1.5B-shaped Qwen2Model, {layers} layers, random weights, fp32 master "
+                        "weights under bf16 autocast, q/v projections trainable, forward + backward on "
+                        "8 rows padded to 1024 tokens (lengths U[512, 1024], seed 0): the patched "
+                        "packed forward against HF's original forward (sdpa) on the same GPU",
+            "layers": layers, "tokens": int(lens.sum()), "padded_tokens": 8 * 1024,
+            "ours_ms": round(ours, 3), "hf_original_ms": round(hf, 3), "speedup": round(hf / ours, 2),
+            "hip_launches_per_step": len(names), "kernels": sorted(set(names))}
+
+
 def kernel_rooflines(body, reps):
     """Per-launch time of each entry point: a graph of one launch per layer of that kernel
     alone (distinct tensors, as in the sweep), replayed `reps` times, timed with HIP events
@@ -704,6 +776,8 @@ def main():
     ap.add_argument("--no-config5", action="store_true", help="skip the config 5 stress line")
     ap.add_argument("--no-attention", action="store_true", help="skip the attention measurement")
     ap.add_argument("--no-lm-head", action="store_true", help="skip the fused LM head measurement")
+    ap.add_argument("--no-packed", action="store_true",
+                    help="skip the end-to-end packed decoder against HF's original forward")
     ap.add_argument("--pmc-kernel", choices=["rmsnorm_fwd", "rmsnorm_bwd", "rope_fwd", "rope_bwd"],
                     help="counter-collection run: a calibration copy of 256 MiB (read 256 MiB, "
                          "write 256 MiB) three times, then one launch per layer of this kernel "
@@ -783,6 +857,7 @@ def main():
     lora = run_lora_dropout(dev, max(args.steps // 3, 5))
     nf4 = run_nf4(dev, max(args.steps // 3, 5))
     lmh = None if args.no_lm_head else run_lm_head(dev, max(args.steps // 3, 5))
+    pdec = None if args.no_packed else run_packed_decoder(dev, 5)
 
     cpu = None
     if not args.no_cpu:
@@ -816,6 +891,7 @@ def main():
         "lora_dropout": lora,
         "nf4_dequant": nf4,
         "lm_head": lmh,
+        "packed_decoder": pdec,
     }
     print(json.dumps(out), flush=True)
     return 0
