@@ -163,8 +163,11 @@ def test_attention_workspace_size():
     assert ws(0, 12, 2, 128) == 0 and ws(8, 3, 2, 128) == 0
     # 1 sequence of 65536 tokens, 28/4 heads: 256-key blocks already fill the GPU, no split
     assert ws(65536, 28, 4, 128) == 28 * 65536
-    # 8192 tokens, 12/2 heads: 32 x 2 blocks, split over all 6 query heads of a kv head
-    assert ws(8192, 12, 2, 128) == 12 * 8192 + 2 * 6 * 8192 * 2 * 128
+    # 8192 tokens, 12/2 heads: 32 x 2 blocks; the smallest divisor s of the 6 query heads of a
+    # kv head with 64 s >= 192 blocks is 3
+    assert ws(8192, 12, 2, 128) == 12 * 8192 + 2 * 3 * 8192 * 2 * 128
+    # 4096 tokens: 16 x 2 blocks, s = 6 (32 x 6 = 192)
+    assert ws(4096, 12, 2, 128) == 12 * 4096 + 2 * 6 * 4096 * 2 * 128
     assert ws(3, 1, 1, 64) == 4  # delta rounded up to a multiple of 4 floats
 
 
