@@ -62,12 +62,13 @@ def rope_bytes(T, HQ, HK, D, e):
 class Body:
     """Resident tensors of the whole sweep and the launch sequence of one step."""
 
-    def __init__(self, cfg, save_rstd, dev):
+    def __init__(self, cfg, save_rstd, dev, batched_dgamma=False):
         import torch
 
         from solution.body import _hip
 
         self.hip, self.cfg, self.save_rstd = _hip, cfg, save_rstd
+        self.batched_dgamma = batched_dgamma
         L, B, S, H, HQ, HK, D = (cfg[k] for k in ("layers", "B", "S", "H", "HQ", "HK", "D"))
         T = B * S
         self.T = T
@@ -89,6 +90,10 @@ class Body:
         self.dx = [torch.empty(T, H, device=dev, dtype=bf) for _ in range(n_norms)]
         self.dw = [torch.empty(H, device=dev) for _ in range(n_norms)]
         self.ws = torch.empty(max(_hip.rmsnorm_partials(T, H), 1), H, device=dev)
+        # batched stage 2: every norm backward of the sweep keeps its own partials, and one
+        # launch after the sweep reduces all of them (esep_dgamma_reduce_batch)
+        self.parts = ([torch.empty(_hip.rmsnorm_partials(T, H), H, device=dev) for _ in range(n_norms)]
+                      if batched_dgamma else None)
         self.q = [rn(B, S, HQ, D) for _ in range(L)]
         self.k = [rn(B, S, HK, D) for _ in range(L)]
         self.qo = [torch.empty_like(t) for t in self.q]
@@ -104,6 +109,10 @@ class Body:
         self.hip.rmsnorm_fwd(self.x[i], self.w[i], self.y[i], self.cfg["eps"], rstd=self.rstd[i])
 
     def norm_bwd(self, i):
+        if self.batched_dgamma:
+            self.hip.rmsnorm_bwd([self.dy[i]], self.x[i], self.w[i], self.cfg["eps"],
+                                 rstd=self.rstd[i], dx=self.dx[i], partials=self.parts[i])
+            return
         self.hip.rmsnorm_bwd([self.dy[i]], self.x[i], self.w[i], self.cfg["eps"],
                              rstd=self.rstd[i], dx=self.dx[i], dw=self.dw[i], workspace=self.ws)
 
@@ -127,6 +136,8 @@ class Body:
             self.norm_bwd(2 * l + 1)
             self.rope_bwd(l)
             self.norm_bwd(2 * l)
+        if self.batched_dgamma:
+            self.hip.dgamma_reduce_batch(self.parts, self.dw)
 
     def step_bytes(self):
         c, T, e = self.cfg, self.T, 2
@@ -239,6 +250,29 @@ def run_config5(dev, steps):
             "ms_per_step": round(ms, 4), "GB/s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4),
             "tokens_per_s": round(CFG5["T"] / (ms * 1e-3), 1), "bytes_per_step": total,
             "kernels": kernels}
+
+
+def run_config4_batched_dgamma(dev, steps, save_rstd):
+    """Config 4's step with the weight-gradient stage 2 batched: the 57 norm backwards of the sweep
+    write their own partials and one esep_dgamma_reduce_batch launch after the sweep sums all of
+    them (the same bits as one reduce per norm). Same bytes; 56 launches fewer per step."""
+    import torch
+
+    body = Body(CFG4, save_rstd, dev, batched_dgamma=True)
+    torch.cuda.synchronize()
+    g = capture(body.step)
+    time_graph(g, 2)
+    ev_ms, wall_ms = time_graph(g, steps)
+    ms = max(ev_ms, wall_ms)
+    nbytes = body.step_bytes()
+    gbs = nbytes / (ms * 1e-3) / 1e9
+    log(f"config 4, batched weight-gradient stage 2: {ms:.3f} ms per step, {gbs:.0f} GB/s = "
+        f"{gbs / PEAK_GBS:.1%} of peak")
+    del g, body
+    torch.cuda.empty_cache()
+    return {"schedule": "norm backwards write partials; one esep_dgamma_reduce_batch after the sweep",
+            "ms_per_step": round(ms, 4), "GB/s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4),
+            "launches_per_step": 4 * CFG4["layers"] + 2 + 2 * CFG4["layers"] + 1}
 
 
 def run_config4_other_rstd(dev, steps, save_rstd):
@@ -850,6 +884,7 @@ def main():
     del body
     torch.cuda.empty_cache()
     c4_other = run_config4_other_rstd(dev, max(args.steps // 3, 5), not save_rstd)
+    c4_batched = run_config4_batched_dgamma(dev, max(args.steps // 3, 5), save_rstd)
     c5 = None if args.no_config5 else run_config5(dev, max(args.steps // 3, 5))
     api = run_api_variant(dev, max(args.steps // 3, 5))
     attn = None if args.no_attention else run_attention(dev, max(args.steps // 3, 5))
@@ -884,6 +919,7 @@ def main():
         "roofline": roofline,
         "cpu_baseline": cpu,
         "config4_other_rstd": c4_other,
+        "config4_batched_dgamma": c4_batched,
         "config5": c5,
         "api_variant": api,
         "attention": attn,

@@ -302,6 +302,34 @@ int esep_dgamma_reduce(const float* partials, int64_t n_partials, int64_t n, voi
   return e == hipSuccess ? 0 : hip_fail(e, "dgamma_reduce launch");
 }
 
+int esep_dgamma_reduce_batch(const esep_dgamma_item* items, int n_items, int64_t n, int dw_dt,
+                             void* stream) {
+  g_err[0] = 0;
+  static_assert(ESEP_DGAMMA_BATCH_MAX == esep::kDgammaBatchMax, "batch limit mismatch");
+  if (items == nullptr || n_items < 1 || n_items > ESEP_DGAMMA_BATCH_MAX)
+    return fail(ESEP_EINVAL, "dgamma_reduce_batch: n_items=%d outside [1, %d] or no items",
+                n_items, ESEP_DGAMMA_BATCH_MAX);
+  if (n < 1 || n > ESEP_NORM_MAX_COLS)
+    return fail(ESEP_ESHAPE, "dgamma_reduce_batch: n=%lld outside [1, %d]", (long long)n,
+                ESEP_NORM_MAX_COLS);
+  if (!float_dt(dw_dt)) return fail(ESEP_EINVAL, "dgamma_reduce_batch: dw needs a float dtype");
+  esep::DgammaBatch b = {};
+  for (int i = 0; i < n_items; ++i) {
+    const esep_dgamma_item& it = items[i];
+    if (it.n_partials < 0)
+      return fail(ESEP_ESHAPE, "dgamma_reduce_batch: item %d has n_partials < 0", i);
+    if (it.dw == nullptr || (it.n_partials > 0 && it.partials == nullptr))
+      return fail(ESEP_EINVAL, "dgamma_reduce_batch: item %d needs dw and its partials", i);
+    b.part[i] = it.partials;
+    b.P[i] = it.n_partials;
+    b.dw[i] = it.dw;
+  }
+  bool sup = false;
+  const hipError_t e = esep::launch_dgamma_reduce_batch(b, n_items, (int)n, dw_dt,
+                                                        static_cast<hipStream_t>(stream), &sup);
+  return e == hipSuccess ? 0 : hip_fail(e, "dgamma_reduce_batch launch");
+}
+
 int esep_rope(const void* q, const int64_t q_strides[3], const void* q_delta,
               const int64_t qd_strides[3], const void* k, const int64_t k_strides[3], void* q_out,
               const int64_t qo_strides[3], void* k_out, const int64_t ko_strides[3], int dt,

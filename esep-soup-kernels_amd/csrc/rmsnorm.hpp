@@ -699,9 +699,12 @@ __global__ __launch_bounds__(kBwdThreads) void k_rmsnorm_bwd(const BwdArgs a) {
 constexpr int kRedCols = 16;
 constexpr int kRedStripes = 64;
 
+// Stage 2 for columns [blockIdx.x * kRedCols, + kRedCols) of one [P, n] partials array: 64
+// stripes of rows summed per thread, then a fixed tree over the stripes. Shared by the
+// single-norm and the batched kernel, so both give the same bits for the same partials.
 template <typename TW>
-__global__ __launch_bounds__(256) void k_dgamma_reduce(const float* __restrict__ part,
-                                                          int64_t P, int n, TW* __restrict__ dw) {
+__device__ __forceinline__ void dgamma_reduce_cols(const float* __restrict__ part, int64_t P,
+                                                   int n, TW* __restrict__ dw) {
   __shared__ f32x4 red[kRedStripes][kRedCols / 4];
   const int c = threadIdx.x % (kRedCols / 4);
   const int r = threadIdx.x / (kRedCols / 4);
@@ -738,6 +741,25 @@ __global__ __launch_bounds__(256) void k_dgamma_reduce(const float* __restrict__
   }
 }
 
+template <typename TW>
+__global__ __launch_bounds__(256) void k_dgamma_reduce(const float* __restrict__ part,
+                                                          int64_t P, int n, TW* __restrict__ dw) {
+  dgamma_reduce_cols<TW>(part, P, n, dw);
+}
+
+// Several norms' stage 2 in one launch: blockIdx.y selects the item.
+constexpr int kDgammaBatchMax = 64;
+struct DgammaBatch {
+  const float* part[kDgammaBatchMax];
+  int64_t P[kDgammaBatchMax];
+  void* dw[kDgammaBatchMax];
+};
+template <typename TW>
+__global__ __launch_bounds__(256) void k_dgamma_reduce_batch(const DgammaBatch b, int n) {
+  const int i = blockIdx.y;
+  dgamma_reduce_cols<TW>(b.part[i], b.P[i], n, static_cast<TW*>(b.dw[i]));
+}
+
 // Launch helpers implemented in the instantiating translation units.
 hipError_t launch_rmsnorm_fwd(const FwdArgs& a, int x_dt, int d_dt, int y_dt, int nv, dim3 grid,
                               dim3 block, hipStream_t s, bool* supported);
@@ -745,5 +767,7 @@ hipError_t launch_rmsnorm_bwd(const BwdArgs& a, int x_dt, int dy_dt, int o_dt, i
                               dim3 block, size_t lds_bytes, hipStream_t s, bool* supported);
 hipError_t launch_dgamma_reduce(const float* part, int64_t P, int n, void* dw, int dw_dt,
                                 hipStream_t s, bool* supported);
+hipError_t launch_dgamma_reduce_batch(const DgammaBatch& b, int count, int n, int dw_dt,
+                                      hipStream_t s, bool* supported);
 
 }  // namespace esep

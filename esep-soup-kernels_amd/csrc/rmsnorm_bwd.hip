@@ -82,4 +82,21 @@ hipError_t launch_dgamma_reduce(const float* part, int64_t P, int n, void* dw, i
   return hipGetLastError();
 }
 
+hipError_t launch_dgamma_reduce_batch(const DgammaBatch& b, int count, int n, int dw_dt,
+                                      hipStream_t s, bool* sup) {
+  *sup = true;
+  const dim3 grid((n + kRedCols - 1) / kRedCols, count), block(256);
+  if (dw_dt == 0)
+    hipLaunchKernelGGL(k_dgamma_reduce_batch<float>, grid, block, 0, s, b, n);
+  else if (dw_dt == 1)
+    hipLaunchKernelGGL(k_dgamma_reduce_batch<_Float16>, grid, block, 0, s, b, n);
+  else if (dw_dt == 2)
+    hipLaunchKernelGGL(k_dgamma_reduce_batch<__bf16>, grid, block, 0, s, b, n);
+  else {
+    *sup = false;
+    return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
 }  // namespace esep

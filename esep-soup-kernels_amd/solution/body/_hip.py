@@ -42,6 +42,7 @@ SIGNATURES = {
                                 _vp, _i32, _vp, _vp, _i32, _i64, _vp, _i64, _vp, _i32, _i64, _i64,
                                 _f32, _vp]),
     "esep_dgamma_reduce": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp]),
+    "esep_dgamma_reduce_batch": (_i32, [_vp, _i32, _i64, _i32, _vp]),
     "esep_attn_fwd": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i32, _i64, _i32,
                              _i32, _i32, _vp, _i32, _i32, _f32, _vp]),
     "esep_attn_bwd_workspace": (_i64, [_i64, _i32, _i32, _i32]),
@@ -253,6 +254,34 @@ def dgamma_reduce(partials, dw):
     rc = lib().esep_dgamma_reduce(_p(partials) if P else None, P, n, _p(dw), dtype_code(dw.dtype),
                                   _stream(dev))
     _check(rc, "esep_dgamma_reduce")
+
+
+class DgammaItem(ctypes.Structure):
+    """esep_dgamma_item (include/esep_body.h)."""
+    _fields_ = [("partials", _vp), ("n_partials", _i64), ("dw", _vp)]
+
+
+DGAMMA_BATCH_MAX = 64
+
+
+def dgamma_reduce_batch(partials, dws):
+    """Stage 2 of several norms in one launch (esep_dgamma_reduce_batch): dws[i] gets exactly
+    what dgamma_reduce(partials[i], dws[i]) would write. partials: fp32 [P_i, n] contiguous
+    tensors (P_i may differ), dws: contiguous [n] tensors of one float dtype."""
+    if len(partials) != len(dws) or not 1 <= len(dws) <= DGAMMA_BATCH_MAX:
+        raise EsepError(f"1..{DGAMMA_BATCH_MAX} (partials, dw) pairs per launch")
+    dev = _dev(*partials, *dws)
+    n = dws[0].numel()
+    arr = (DgammaItem * len(dws))()
+    for i, (part, dw) in enumerate(zip(partials, dws)):
+        if part.dtype != torch.float32 or not part.is_contiguous() or part.dim() != 2:
+            raise EsepError("partials must be contiguous fp32 [P, n] tensors")
+        if part.shape[1] != n or dw.numel() != n or not dw.is_contiguous() or dw.dtype != dws[0].dtype:
+            raise EsepError(f"every dw must be a contiguous [{n}] tensor of one dtype")
+        arr[i] = DgammaItem(_p(part) if part.shape[0] else None, part.shape[0], _p(dw))
+    rc = lib().esep_dgamma_reduce_batch(ctypes.cast(arr, _vp), len(dws), n, dtype_code(dws[0].dtype),
+                                        _stream(dev))
+    _check(rc, "esep_dgamma_reduce_batch")
 
 
 def rope(q, k, qo, ko, inv_freq, sign, q_delta=None, positions=None, cu_seqlens=None,

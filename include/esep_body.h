@@ -138,6 +138,24 @@ int esep_dgamma_reduce(const float* partials, int64_t n_partials, int64_t n, voi
                        void* stream);
 
 /*
+ * Stage 2 for several norms in one launch: for each item i, dw_i[j] = sum_p partials_i[p, j]
+ * exactly as esep_dgamma_reduce computes it (bitwise the same dw_i). No reference counterpart
+ * (the reference computes no weight gradient); for a training step whose norm-weight gradients
+ * are read only after the backward sweep: the sweep's norm backwards write their partials
+ * (dw == NULL, each its own buffer) and one launch reduces them all instead of one launch per
+ * norm. All items share n and dw_dt; `items` is a host array of 1 .. ESEP_DGAMMA_BATCH_MAX
+ * entries, read during the call (copied into the launch).
+ */
+#define ESEP_DGAMMA_BATCH_MAX 64
+typedef struct {
+  const float* partials; /* fp32 [n_partials, n] contiguous (NULL only when n_partials == 0) */
+  int64_t n_partials;
+  void* dw;              /* [n] of dw_dt */
+} esep_dgamma_item;
+int esep_dgamma_reduce_batch(const esep_dgamma_item* items, int n_items, int64_t n, int dw_dt,
+                             void* stream);
+
+/*
  * Rotary embedding on q and k in one launch (forward with sin_sign = +1, backward with -1).
  * Replaces the launch of _rope_kernel at solution/body/norm_rope.py:388-392 (_launch_rope);
  * kernel math follows norm_rope.py:330-369 (rotate_half convention of HF apply_rotary_pos_emb).

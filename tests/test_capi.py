@@ -88,6 +88,31 @@ def test_dgamma_reduce_validation():
     assert lib.esep_dgamma_reduce(1, 4, 8, 1, 3, None) == -1 and b"dgamma" in lib.esep_last_error()
 
 
+def test_dgamma_reduce_batch_validation():
+    """esep_dgamma_reduce_batch checks the item count, n, the dtype and every item's pointers and
+    partial count before launching anything."""
+    lib = _hip.lib()
+
+    def call(n_items=2, n=8, dt=0, **kw):
+        arr = (_hip.DgammaItem * 65)()
+        for i in range(65):
+            f = dict(partials=64, n_partials=4, dw=64)
+            if i == 1:
+                f.update(kw)
+            arr[i] = _hip.DgammaItem(*f.values())
+        return lib.esep_dgamma_reduce_batch(ctypes.cast(arr, ctypes.c_void_p), n_items, n, dt, None)
+
+    assert call(n_items=0) == -1 and call(n_items=65) == -1
+    assert lib.esep_dgamma_reduce_batch(None, 1, 8, 0, None) == -1
+    assert call(n=0) == -2 and call(n=16385) == -2
+    assert call(dt=3) == -1
+    assert call(dw=None) == -1 and b"item 1" in lib.esep_last_error()
+    assert call(partials=None) == -1
+    assert call(n_partials=-1) == -2
+    assert _hip.DGAMMA_BATCH_MAX == int(re.search(r"#define ESEP_DGAMMA_BATCH_MAX (\d+)",
+                                                  HEADER.read_text()).group(1))
+
+
 def test_rope_validation():
     lib = _hip.lib()
     S3 = ctypes.c_int64 * 3

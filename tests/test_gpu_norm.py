@@ -432,6 +432,39 @@ def test_dgamma_partials_then_reduce(T, n):
     assert torch.equal(z, torch.zeros_like(z))
 
 
+def test_dgamma_reduce_batch_matches_per_norm():
+    """One batched stage-2 launch over several norms' partials (different row counts, so different
+    partial counts, plus an empty one) writes each dw bit for bit as its own esep_dgamma_reduce;
+    fp32 and bf16 dw."""
+    from solution.body import _hip
+
+    n = 1536
+    g = gen(11)
+    w = (1 + 0.02 * torch.randn(n, generator=g)).to(DEV)
+    parts = []
+    for T in (8192, 300, 1, 4097):
+        x = randn((T, n), g, dtype=torch.bfloat16)
+        dy = randn((T, n), g, dtype=torch.bfloat16)
+        part = torch.empty((_hip.rmsnorm_partials(T, n), n), device=DEV)
+        _hip.rmsnorm_bwd([dy], x, w, EPS, dx=torch.empty_like(x), partials=part)
+        parts.append(part)
+    parts.append(torch.empty((0, n), device=DEV))
+    for dt in (torch.float32, torch.bfloat16):
+        one = [torch.full((n,), float("nan"), device=DEV, dtype=dt) for _ in parts]
+        batch = [torch.full((n,), float("nan"), device=DEV, dtype=dt) for _ in parts]
+        for p, d in zip(parts, one):
+            _hip.dgamma_reduce(p, d)
+        _hip.dgamma_reduce_batch(parts, batch)
+        for a, b in zip(one, batch):
+            assert torch.equal(a, b)
+        assert torch.equal(batch[-1], torch.zeros_like(batch[-1]))
+    # the first norm's dw against the float64 oracle sum of its partials
+    ref64 = parts[0].double().sum(0)
+    got = torch.empty(n, device=DEV)
+    _hip.dgamma_reduce_batch(parts[:1], [got])
+    assert (got.double() - ref64).abs().max() <= 1e-5 * ref64.abs().max()
+
+
 def test_add_rmsnorm_weight_grad():
     """A trainable weight gets dw in its own dtype (bf16 weight -> bf16 grad) = sum dy * xhat."""
     nr = _nr()
