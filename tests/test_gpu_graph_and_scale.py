@@ -1,7 +1,7 @@
 """HIP-graph capture of the C-ABI launches, and the config-5 stress shape at full size.
 
-Graphs: the norm forward, the norm backward with its weight-gradient reduction and both RoPE
-directions, captured once and replayed several times with other GPU work and host syncs in
+Graphs: the norm forward, the norm backward with its weight-gradient reduction (per call, and
+two calls' partials reduced by one batched launch) and both RoPE directions, captured once and replayed several times with other GPU work and host syncs in
 between; every replay must equal the eager launches bit for bit (the library records no
 memset and allocates nothing, so replays are self-contained).
 
@@ -38,22 +38,31 @@ def test_graph_replays_match_eager():
     inv = (1.0 / (1e6 ** (torch.arange(0, D, 2, dtype=torch.float) / D))).to(DEV)
     cu = torch.tensor([0, 1000, 1001, 3000, T], dtype=torch.int32, device=DEV)
     ws = torch.empty(_hip.rmsnorm_partials(T, H), H, device=DEV)
+    # two norm backwards keeping their partials, reduced by one batched launch
+    dy2 = rn(T, H)
+    parts = [torch.empty(_hip.rmsnorm_partials(T, H), H, device=DEV) for _ in range(2)]
 
     def outputs():
         return dict(y=torch.empty_like(x), rstd=torch.empty(T, device=DEV),
                     dx=torch.empty_like(x), dw=torch.empty(H, device=DEV),
                     qo=torch.empty_like(q), ko=torch.empty_like(k),
-                    dq=torch.empty_like(q), dk=torch.empty_like(k))
+                    dq=torch.empty_like(q), dk=torch.empty_like(k),
+                    dx2=torch.empty_like(x), dwb0=torch.empty(H, device=DEV),
+                    dwb1=torch.empty(H, device=DEV))
 
     def run(o):
         _hip.rmsnorm_fwd(x, w, o["y"], EPS, rstd=o["rstd"])
         _hip.rmsnorm_bwd([dy], x, w, EPS, rstd=o["rstd"], dx=o["dx"], dw=o["dw"], workspace=ws)
         _hip.rope(q, k, o["qo"], o["ko"], inv, 1.0, cu_seqlens=cu)
         _hip.rope(dq_in, dk_in, o["dq"], o["dk"], inv, -1.0, cu_seqlens=cu)
+        _hip.rmsnorm_bwd([dy], x, w, EPS, rstd=o["rstd"], dx=o["dx"], partials=parts[0])
+        _hip.rmsnorm_bwd([dy2], x, w, EPS, rstd=o["rstd"], dx=o["dx2"], partials=parts[1])
+        _hip.dgamma_reduce_batch(parts, [o["dwb0"], o["dwb1"]])
 
     eager = outputs()
     run(eager)
     torch.cuda.synchronize()
+    assert torch.equal(eager["dwb0"], eager["dw"])  # batched stage 2 == the fused call's
     graphed = outputs()
     s = torch.cuda.Stream()
     s.wait_stream(torch.cuda.current_stream())
