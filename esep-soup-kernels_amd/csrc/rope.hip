@@ -18,7 +18,11 @@
 
 namespace esep {
 
-constexpr int kRopeWaves = 4;
+// Wavefronts per block: 4 with two tokens per wavefront, 2 with one. Measured per launch (us,
+// fwd / bwd): config 4 (two tokens) 2 waves 10.62 / 10.66, 4 waves 10.57 / 10.56, 8 waves
+// 10.59 / 10.64; config 5 (one token) 2 waves 184.4 / 182.6, 4 waves 189.2 / 187.9, 8 waves
+// 188.3 / 187.4.
+constexpr int rope_waves(int tpw) { return tpw == 2 ? 4 : 2; }
 constexpr int kRopePasses = 4;
 
 // One head half (8 elements) of one lane: VEC as a single raw 16-byte (two for fp32)
@@ -185,12 +189,13 @@ __device__ __forceinline__ void rope_store(const RopeArgs& a, const int64_t (&bb
 }
 
 template <typename T, int HALF, bool VEC, bool QD, int TPW>
-__global__ __launch_bounds__(kRopeWaves * kWave) void k_rope(const RopeArgs a) {
-  __shared__ float cs[kRopeWaves][TPW][2][HALF];
+__global__ __launch_bounds__(rope_waves(TPW) * kWave) void k_rope(const RopeArgs a) {
+  constexpr int NW = rope_waves(TPW);
+  __shared__ float cs[NW][TPW][2][HALF];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int64_t tokens = a.B * a.S;
-  const int64_t t0 = ((int64_t)blockIdx.x * kRopeWaves + wave) * TPW;
+  const int64_t t0 = ((int64_t)blockIdx.x * NW + wave) * TPW;
   if (t0 >= tokens) return;  // whole wavefront leaves; nothing below waits on other waves
   int64_t bb[TPW], ss[TPW];
   bool live[TPW];
@@ -254,8 +259,9 @@ static void rope_variant(const RopeArgs& a, hipStream_t s) {
   const int64_t tokens = a.B * a.S;
   const int passes = (a.HQ + a.HK + HPP - 1) / HPP;
   const int tpw = (a.vec && passes <= 2) ? 2 : 1;
-  const dim3 b(kRopeWaves * kWave);
-  const dim3 g((unsigned)((tokens + kRopeWaves * tpw - 1) / (kRopeWaves * tpw)));
+  const int nw = rope_waves(tpw);
+  const dim3 b(nw * kWave);
+  const dim3 g((unsigned)((tokens + nw * tpw - 1) / (nw * tpw)));
   if (a.vec) {
     if (tpw == 2 && !qd) hipLaunchKernelGGL((k_rope<T, HALF, true, false, 2>), g, b, 0, s, a);
     else if (tpw == 2) hipLaunchKernelGGL((k_rope<T, HALF, true, true, 2>), g, b, 0, s, a);
