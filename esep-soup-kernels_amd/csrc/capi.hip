@@ -200,6 +200,8 @@ int esep_rmsnorm_bwd(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
   if (dw != nullptr && (!float_dt(dw_dt) || dw_partials == nullptr))
     return fail(ESEP_EINVAL, "rmsnorm_bwd: dw needs dw_partials and a float dtype");
   if (dw_partials != nullptr) {
+    if (!aligned16(dw_partials))
+      return fail(ESEP_EALIGN, "rmsnorm_bwd: dw_partials must be 16-byte aligned");
     const int64_t want = esep_rmsnorm_partials(rows, n);
     if (rows > 0 && n_partials != want)
       return fail(ESEP_ESHAPE, "rmsnorm_bwd: n_partials=%lld, this shape needs %lld",
@@ -259,7 +261,6 @@ int esep_rmsnorm_bwd(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
   if (dr_f32) vec = vec && aligned16(dr_f32);
   if (dx_lp) vec = vec && aligned16(dx_lp) && ld_ok(ld_out, dx_dt);
   if (dr_out || dr_f32) vec = vec && ld_ok(ld_out, ESEP_F32);
-  if (a.part) vec = vec && aligned16(dw_partials);
   if (n_special > 0) vec = vec && aligned16(slot);
   a.vec = vec ? 1 : 0;
 
@@ -296,6 +297,8 @@ int esep_dgamma_reduce(const float* partials, int64_t n_partials, int64_t n, voi
   if (n_partials < 0) return fail(ESEP_ESHAPE, "dgamma_reduce: n_partials < 0");
   if (dw == nullptr || !float_dt(dw_dt) || (n_partials > 0 && partials == nullptr))
     return fail(ESEP_EINVAL, "dgamma_reduce: dw, its float dtype and the partials are required");
+  if (n_partials > 0 && !aligned16(partials))
+    return fail(ESEP_EALIGN, "dgamma_reduce: partials must be 16-byte aligned");
   bool sup = false;
   const hipError_t e = esep::launch_dgamma_reduce(partials, n_partials, (int)n, dw, dw_dt,
                                                   static_cast<hipStream_t>(stream), &sup);
@@ -320,6 +323,8 @@ int esep_dgamma_reduce_batch(const esep_dgamma_item* items, int n_items, int64_t
       return fail(ESEP_ESHAPE, "dgamma_reduce_batch: item %d has n_partials < 0", i);
     if (it.dw == nullptr || (it.n_partials > 0 && it.partials == nullptr))
       return fail(ESEP_EINVAL, "dgamma_reduce_batch: item %d needs dw and its partials", i);
+    if (it.n_partials > 0 && !aligned16(it.partials))
+      return fail(ESEP_EALIGN, "dgamma_reduce_batch: item %d's partials are not 16-byte aligned", i);
     b.part[i] = it.partials;
     b.P[i] = it.n_partials;
     b.dw[i] = it.dw;

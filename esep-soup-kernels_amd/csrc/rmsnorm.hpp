@@ -692,19 +692,22 @@ __global__ __launch_bounds__(kBwdThreads) void k_rmsnorm_bwd(const BwdArgs a) {
     bwd_rows<NV, VEC, TX, TDY, TO>(a, red, lds);
 }
 
-// Stage 2 of the weight gradient: dw[j] = sum_p part[p, j]. A block of 256 threads owns 16
-// columns: thread (stripe r = tid / 4, quad c = tid % 4) adds the 4 columns 4c..4c+3 of rows
-// p = r, r + 64, r + 128, ... in ascending p, then a fixed 6-level tree adds the 64 stripe
+// Stage 2 of the weight gradient: dw[j] = sum_p part[p, j]. A block of 256 threads owns
+// kRedCols columns: thread (stripe r = tid / (kRedCols / 4), quad c = tid % (kRedCols / 4)) adds
+// the 4 columns 4c..4c+3 of the block's span over rows p = r, r + kRedStripes, r + 2 kRedStripes,
+// ... in ascending p, then a fixed tree of log2(kRedStripes) levels adds the kRedStripes stripe
 // sums (stripe r + h into stripe r). n % 4 != 0 takes the same order one column at a time.
-// Stage-2 block shape: kRedCols columns x kRedStripes row stripes over 256 threads. Measured at
-// config 4 (per call with its reduce / batched over 57 norms, us per norm): 8 x 128 19.9 / 17.1,
-// 16 x 64 18.9 / 16.7, 32 x 32 18.8 / 16.4, 64 x 16 19.4 / 16.4.
+// Block shape kRedCols x kRedStripes, measured at config 4 (per call with its reduce / batched
+// over 57 norms, us per norm): 8 x 128 19.9 / 17.1, 16 x 64 18.9 / 16.7, 32 x 32 18.8 / 16.4,
+// 64 x 16 19.4 / 16.4.
 constexpr int kRedCols = 32;
 constexpr int kRedStripes = 1024 / kRedCols;
 
-// Stage 2 for columns [blockIdx.x * kRedCols, + kRedCols) of one [P, n] partials array: 64
-// stripes of rows summed per thread, then a fixed tree over the stripes. Shared by the
-// single-norm and the batched kernel, so both give the same bits for the same partials.
+// Stage 2 for columns [blockIdx.x * kRedCols, + kRedCols) of one [P, n] partials array:
+// kRedStripes stripes of rows summed per thread, then the fixed tree over the stripes. Shared
+// by the single-norm and the batched kernel, so both give the same bits for the same partials.
+// The partials are read as 16-byte vectors when n % 4 == 0 (the entry points require 16-byte
+// aligned partials).
 template <typename TW>
 __device__ __forceinline__ void dgamma_reduce_cols(const float* __restrict__ part, int64_t P,
                                                    int n, TW* __restrict__ dw) {

@@ -152,10 +152,15 @@ def _stream(dev):
 
 
 def _rows_ld(t, n):
-    """Leading dimension of a [rows, n] tensor whose last dim is contiguous."""
-    if t.dim() != 2 or t.shape[1] != n or (t.shape[0] > 1 and t.stride(1) != 1):
+    """Leading dimension of a [rows, n] tensor whose last dim is contiguous. The column stride
+    is checked whenever a row has more than one element (a one-row view such as t[:, ::2] or an
+    expanded row has a non-unit column stride too); a multi-row tensor must not overlap its
+    rows (row stride >= n, so an expanded stride 0 is rejected)."""
+    if t.dim() != 2 or t.shape[1] != n or (n > 1 and t.stride(1) != 1):
         raise EsepError(f"expected a [rows, {n}] tensor with unit column stride, got "
                         f"{tuple(t.shape)} / {t.stride()}")
+    if t.shape[0] > 1 and t.stride(0) < n:
+        raise EsepError(f"rows of a [rows, {n}] tensor overlap (row stride {t.stride(0)})")
     return t.stride(0) if t.shape[0] > 1 else n
 
 

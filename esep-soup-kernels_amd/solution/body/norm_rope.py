@@ -34,7 +34,7 @@ rmsnorm(x, weight, eps, out_dtype=None, recompute_rstd=False) -> y
     requires a gradient, rstd saved or recomputed in backward.
 """
 
-import weakref
+import math
 
 import torch
 
@@ -49,33 +49,38 @@ MAX_DY = 5
 SPECIAL_W_MIN = 2.0 ** -10
 
 _FLOATS = (torch.float32, torch.float16, torch.bfloat16)
-_SPECIAL = {}  # (device, data_ptr, version, n, dtype, threshold) -> (weakref, slots, K)
+
+# Attribute under which special_channels memoizes its answer on the weight tensor itself.
+_MEMO_ATTR = "_esep_exact_channels"
 
 
 def special_channels(weight):
     """(slots int32 [H], K) for a frozen norm weight [H]: slots[j] = 0..K-1 (ascending channel
-    order) for the channels whose xhat is saved exactly, -1 elsewhere. One host sync per new
-    weight; cached on (storage, version counter, shape, dtype) with a weak reference, so an
-    in-place edit recomputes it and a new tensor at a reused address is not mistaken for it.
-    Reference: norm_rope.py:183-205."""
+    order) for the channels whose xhat is saved exactly, -1 elsewhere. Reference:
+    norm_rope.py:183-205.
+
+    A channel is well-conditioned for the y / w recovery when SPECIAL_W_MIN <= |w| <=
+    65504 / sqrt(H); every other channel (tiny, huge, NaN or infinite weight) is exact. The
+    answer is memoized on the weight tensor, tagged with its storage address, version counter,
+    size, dtype and the threshold in force: an in-place edit (which bumps the version) or a
+    new threshold recomputes it, and the memo dies with the tensor. Computing it costs one
+    host sync (the count K)."""
     thr = float(SPECIAL_W_MIN)
-    key = (weight.device, weight.data_ptr(), weight._version, weight.shape[0], weight.dtype, thr)
-    hit = _SPECIAL.get(key)
-    if hit is not None and hit[0]() is weight:
-        return hit[1], hit[2]
-    a = weight.detach().to(torch.float32).abs()
-    big = 65504.0 / float(weight.shape[0]) ** 0.5
-    special = (a < thr) | (a > big) | ~torch.isfinite(a)
-    idx = special.nonzero().squeeze(1)
-    k = int(idx.numel())
-    slots = torch.full(a.shape, -1, device=a.device, dtype=torch.int32)
-    if k:
-        slots[idx] = torch.arange(k, device=a.device, dtype=torch.int32)
+    tag = (weight.data_ptr(), weight._version, weight.numel(), weight.dtype, thr)
+    memo = getattr(weight, _MEMO_ATTR, None)
+    if memo is not None and memo[0] == tag:
+        return memo[1], memo[2]
+    mag = weight.detach().to(torch.float32).abs()
+    limit = 65504.0 / math.sqrt(weight.shape[0])
+    exact = ~((mag >= thr) & (mag <= limit))  # NaN fails both comparisons
+    rank = torch.cumsum(exact, 0, dtype=torch.int32) - 1
+    slots = torch.where(exact, rank, torch.full_like(rank, -1))
+    count = int(exact.sum())
     try:
-        _SPECIAL[key] = (weakref.ref(weight), slots, k)
-    except TypeError:  # not weak-referenceable: no cache
+        setattr(weight, _MEMO_ATTR, (tag, slots, count))
+    except (AttributeError, TypeError):  # a tensor subclass without attributes: no memo
         pass
-    return slots, k
+    return slots, count
 
 
 def _weight_f32(weight, grad):
@@ -89,45 +94,55 @@ def _wants_weight_grad(weight):
     return bool(weight.requires_grad and torch.is_grad_enabled())
 
 
+def _rows_of(t, dtype=None):
+    """t [..., n] as a dense [rows, n] tensor (optionally cast): the kernels' row layout."""
+    n = t.shape[-1]
+    flat = t.reshape(-1, n)
+    if dtype is not None and flat.dtype != dtype:
+        flat = flat.to(dtype)
+    return flat.contiguous()
+
+
 class AddRMSNorm(torch.autograd.Function):
-    """Reference: norm_rope.py:208-286 (same apply() arguments and saved tensors)."""
+    """Reference: norm_rope.py:208-286 (same apply() arguments and saved tensors).
+
+    apply(r_in, delta, w, eps, out_dtype, n_out, slots, n_special) -> (r_out, y_1 .. y_n_out)
+
+    Saved for backward: (r_out, rstd, w); with slots given (save-output mode), (y, rstd, w,
+    slots, xs) where xs [rows, K] holds the exact xhat of the K special channels. Outputs whose
+    gradient nothing produces arrive in backward as None (no zero tensors)."""
 
     @staticmethod
     def forward(ctx, r_in, delta, w, eps, out_dtype, n_out, slots, n_special):
         shape = r_in.shape
         n = shape[-1]
-        assert n <= NORM_BLOCK, "row wider than NORM_BLOCK"
-        assert 1 <= n_out <= MAX_DY
-        r_in2 = r_in.reshape(-1, n).to(torch.float32).contiguous()
-        rows = r_in2.shape[0]
-        has_delta = delta is not None
-        if has_delta:
-            delta2 = delta.reshape(-1, n).contiguous()
-            r_out = torch.empty_like(r_in2)
-        else:
-            delta2 = None
-            r_out = r_in2  # r_out is r_in itself: nothing to add
-        y = torch.empty((rows, n), device=r_in.device, dtype=out_dtype)
-        rstd = torch.empty((rows,), device=r_in.device, dtype=torch.float32)
-        from_y = slots is not None
-        k = n_special if from_y else 0
-        xs = torch.empty((rows, k), device=r_in.device, dtype=torch.float32) if k else None
-        if rows > 0:
-            _hip.rmsnorm_fwd(r_in2, w, y, eps, delta=delta2, r_out=r_out if has_delta else None,
-                             rstd=rstd, slot=slots if k else None, xs=xs, n_special=k)
-        if from_y:
-            ctx.save_for_backward(y, rstd, w, slots, xs)
-        else:
-            ctx.save_for_backward(r_out, rstd, w)
-        ctx.from_y, ctx.n_special, ctx.eps = from_y, k, eps
-        ctx.has_delta = has_delta
-        ctx.delta_dtype = delta.dtype if has_delta else None
-        ctx.shape = shape
-        # Unused outputs (the final norm's r_out, a y copy nothing consumed) reach backward as
-        # None: no zero fill, no read.
+        assert n <= NORM_BLOCK, f"row of {n} columns is wider than NORM_BLOCK={NORM_BLOCK}"
+        assert 1 <= n_out <= MAX_DY, f"n_out={n_out} outside 1..{MAX_DY}"
+        resid_in = _rows_of(r_in, torch.float32)
+        rows, dev = resid_in.shape[0], resid_in.device
+        save_y = slots is not None
+        k_exact = n_special if save_y else 0
+
+        y = torch.empty((rows, n), device=dev, dtype=out_dtype)
+        rstd = torch.empty((rows,), device=dev, dtype=torch.float32)
+        xs = torch.empty((rows, k_exact), device=dev, dtype=torch.float32) if k_exact else None
+        # Without a delta the residual passes through unchanged (r_out aliases r_in) and its
+        # gradient comes back to backward as dr_out; with one, the kernel writes the sum.
+        add = None if delta is None else _rows_of(delta)
+        resid_out = resid_in if add is None else torch.empty_like(resid_in)
+        if rows:
+            _hip.rmsnorm_fwd(resid_in, w, y, eps, delta=add,
+                             r_out=None if add is None else resid_out, rstd=rstd,
+                             slot=slots if k_exact else None, xs=xs, n_special=k_exact)
+
+        ctx.save_for_backward(*((y, rstd, w, slots, xs) if save_y else (resid_out, rstd, w)))
+        ctx.from_y, ctx.n_special, ctx.eps, ctx.shape = save_y, k_exact, eps, shape
+        ctx.has_delta = add is not None
+        ctx.delta_dtype = None if delta is None else delta.dtype
         ctx.set_materialize_grads(False)
-        ys = tuple(y.view(*shape[:-1], n) for _ in range(n_out))
-        return (r_out.view(shape),) + ys
+        # One buffer, n_out distinct views: each consumer's gradient reaches backward on its
+        # own and the kernel sums them there.
+        return (resid_out.view(shape),) + tuple(y.view(shape) for _ in range(n_out))
 
     @staticmethod
     def backward(ctx, dr_out, *dys):
@@ -210,7 +225,8 @@ class RMSNorm(torch.autograd.Function):
         n = shape[-1]
         assert n <= NORM_BLOCK, "row wider than NORM_BLOCK"
         x2 = x.reshape(-1, n)
-        if x2.shape[0] > 1 and x2.stride(1) != 1:
+        # the kernels take rows with a unit column stride that do not overlap
+        if (n > 1 and x2.stride(1) != 1) or (x2.shape[0] > 1 and x2.stride(0) < n):
             x2 = x2.contiguous()
         rows = x2.shape[0]
         y = torch.empty((rows, n), device=x.device, dtype=out_dtype)

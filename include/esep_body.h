@@ -45,7 +45,7 @@ enum esep_status {
   ESEP_OK = 0,
   ESEP_EINVAL = -1,   /* bad pointer / dtype / flag combination */
   ESEP_ESHAPE = -2,   /* unsupported or inconsistent size */
-  ESEP_EALIGN = -3    /* reserved: alignment cannot be served */
+  ESEP_EALIGN = -3    /* a buffer that must be 16-byte aligned is not (weight-gradient partials) */
 };
 
 /* Widest row the RMSNorm kernels accept (columns). The reference caps rows at
@@ -110,7 +110,8 @@ int64_t esep_rmsnorm_partials(int64_t rows, int64_t n);
  *   dr_f32 [rows, n] fp32 or NULL  <- dr
  *   dx_lp  [rows, n] dx_dt or NULL <- dr rounded to dx_dt
  *   dw_j   = sum_t dy_tj * xhat_tj             when dw_partials != NULL: stage 1 writes the
- *            partials [P, n] fp32 (P = esep_rmsnorm_partials(rows, n), n_partials must equal P);
+ *            partials [P, n] fp32, 16-byte aligned (P = esep_rmsnorm_partials(rows, n),
+ *            n_partials must equal P; a misaligned buffer returns ESEP_EALIGN);
  *            with dw != NULL stage 2 then sums them in a fixed order into dw [n] (dw_dt), else
  *            the caller reduces them later with esep_dgamma_reduce. rows == 0 gives dw = 0.
  * n_dy == 0 and dr_out != NULL gives dr = dr_out. Contiguous rows for dr_out, dr_f32, dx_lp
@@ -129,7 +130,8 @@ int esep_rmsnorm_bwd(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
 /*
  * Stage 2 of the weight gradient on its own: dw[j] = sum_{p < n_partials} partials[p, j], summed
  * in an order that depends on n_partials only (bitwise equal to the stage 2 inside
- * esep_rmsnorm_bwd for the same partials). partials: fp32 [n_partials, n] contiguous;
+ * esep_rmsnorm_bwd for the same partials). partials: fp32 [n_partials, n] contiguous and
+ * 16-byte aligned (else ESEP_EALIGN);
  * n_partials == 0 writes zeros. No reference counterpart (the reference computes no weight
  * gradient: norm_rope.py:286 returns None for it); for callers that run stage 1 per micro-batch
  * or on several streams and reduce once.
@@ -148,7 +150,8 @@ int esep_dgamma_reduce(const float* partials, int64_t n_partials, int64_t n, voi
  */
 #define ESEP_DGAMMA_BATCH_MAX 64
 typedef struct {
-  const float* partials; /* fp32 [n_partials, n] contiguous (NULL only when n_partials == 0) */
+  const float* partials; /* fp32 [n_partials, n] contiguous, 16-byte aligned (NULL only when
+                            n_partials == 0) */
   int64_t n_partials;
   void* dw;              /* [n] of dw_dt */
 } esep_dgamma_item;

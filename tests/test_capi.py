@@ -72,9 +72,12 @@ def test_rmsnorm_bwd_validation():
     assert bwd(dys=Arr(None)) == -1
     assert bwd(from_y=1) == -1 and b"rstd" in lib.esep_last_error()
     assert bwd(dw=1) == -1  # no partials workspace
-    assert bwd(dw=1, part=1, n_part=3) == -2 and b"needs 1" in lib.esep_last_error()
-    assert bwd(part=1, n_part=3) == -2  # partials only: the count is checked too
-    assert bwd(dw=1, dw_dt=3, part=1, n_part=1) == -1  # int32 dw
+    assert bwd(dw=1, part=64, n_part=3) == -2 and b"needs 1" in lib.esep_last_error()
+    assert bwd(part=64, n_part=3) == -2  # partials only: the count is checked too
+    assert bwd(dw=1, dw_dt=3, part=64, n_part=1) == -1  # int32 dw
+    # the partials are read and written as 16-byte vectors: a misaligned buffer is refused
+    assert bwd(dw=1, part=8, n_part=1) == -3 and b"aligned" in lib.esep_last_error()
+    assert bwd(part=4, n_part=1) == -3
     assert bwd(rows=0) == 0
 
 
@@ -86,6 +89,7 @@ def test_dgamma_reduce_validation():
     assert lib.esep_dgamma_reduce(1, 4, 8, None, 0, None) == -1
     assert lib.esep_dgamma_reduce(None, 4, 8, 1, 0, None) == -1
     assert lib.esep_dgamma_reduce(1, 4, 8, 1, 3, None) == -1 and b"dgamma" in lib.esep_last_error()
+    assert lib.esep_dgamma_reduce(8, 4, 8, 1, 0, None) == -3 and b"aligned" in lib.esep_last_error()
 
 
 def test_dgamma_reduce_batch_validation():
@@ -109,6 +113,7 @@ def test_dgamma_reduce_batch_validation():
     assert call(dw=None) == -1 and b"item 1" in lib.esep_last_error()
     assert call(partials=None) == -1
     assert call(n_partials=-1) == -2
+    assert call(partials=72) == -3 and b"item 1" in lib.esep_last_error()
     assert _hip.DGAMMA_BATCH_MAX == int(re.search(r"#define ESEP_DGAMMA_BATCH_MAX (\d+)",
                                                   HEADER.read_text()).group(1))
 

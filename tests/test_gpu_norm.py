@@ -41,7 +41,10 @@ def ref_add_rmsnorm(r_in, delta, w, out_dtype):
                                   "bf16_delta", "bf16_out"])
 def test_add_rmsnorm(T, case):
     """Reference test_add_rmsnorm (:32-62): r_out exact, y within 2e-3 (16-bit) / 1e-5, grads
-    within 5e-3 / 1e-5 relative, no weight grad for a frozen weight; bf16 cases added."""
+    within 5e-3 / 1e-5 relative; the weight is an nn.Parameter as there (:41) and
+    torch.autograd.grad leaves its .grad None (:62). bf16 cases added. This build's deliberate
+    difference: a backward() through a trainable weight fills w.grad with
+    dw_j = sum_t dy_tj * xhat_tj (the reference detaches the weight), checked last."""
     nr = _nr()
     g = gen(T)
     delta_dtype = {"fp16_delta": torch.float16, "fp32_delta": torch.float32, "no_delta": None,
@@ -53,10 +56,10 @@ def test_add_rmsnorm(T, case):
     delta = None
     if delta_dtype is not None:
         delta = randn((1, T, H), g, dtype=delta_dtype).requires_grad_()
-    w = (1 + 0.1 * torch.randn(H, generator=g)).to(DEV)
+    w = torch.nn.Parameter((1 + 0.1 * torch.randn(H, generator=g)).to(DEV))
 
     r_out, y = nr.add_rmsnorm(r_in, delta, w, EPS, out_dtype)
-    rr, yr = ref_add_rmsnorm(r_in, delta, w, out_dtype)
+    rr, yr = ref_add_rmsnorm(r_in, delta, w.detach(), out_dtype)
     assert r_out.dtype == torch.float32 and y.dtype == out_dtype
     assert r_out.shape == r_in.shape and y.shape == r_in.shape
     torch.testing.assert_close(r_out, rr, rtol=0, atol=0)
@@ -66,21 +69,28 @@ def test_add_rmsnorm(T, case):
     # against the fp64 oracle (the kernel's own contract: one rounding of the exact value)
     d_np = None if delta is None else np64(delta)
     _, y64, rstd64, _ = ref.add_rmsnorm_fwd(np64(r_in)[0], None if d_np is None else d_np[0],
-                                            np64(w), EPS, STORE[out_dtype])
+                                            np64(w.detach()), EPS, STORE[out_dtype])
     assert_close(np64(y)[0], y64, 2e-3 if out_dtype != torch.float32 else 1e-5, 1e-2, "y")
 
     gy = torch.randn(y.shape, generator=g).to(out_dtype).to(DEV)
     gr = torch.randn(r_out.shape, generator=g).to(DEV)
     ins = [r_in] + ([delta] if delta is not None else [])
-    gk = torch.autograd.grad([r_out, y], ins, [gr, gy])
+    gk = torch.autograd.grad([r_out, y], ins, [gr, gy], retain_graph=True)
     gref = torch.autograd.grad([rr, yr], ins, [gr, gy])
     for a, b in zip(gk, gref):
         assert a.dtype == b.dtype
         ae, re = err(np64(a), np64(b))
         lim = 5e-3 if a.dtype != torch.float32 else 1e-5
         assert re < lim, (ae, re)
-    dr64, _ = ref.add_rmsnorm_bwd([np64(gy)[0]], np64(gr)[0], np64(rr)[0], np64(w), EPS)
+    dr64, dw64 = ref.add_rmsnorm_bwd([np64(gy)[0]], np64(gr)[0], np64(rr)[0], np64(w.detach()),
+                                     EPS)
     assert_close(np64(gk[0])[0], dr64, 1e-4, 1e-4, "d_r_in vs fp64")
+    assert w.grad is None  # autograd.grad does not accumulate (reference :62)
+
+    # backward() with the trainable Parameter: its gradient is the kernel's dw
+    torch.autograd.backward([r_out, y], [gr, gy])
+    assert w.grad is not None and w.grad.dtype == torch.float32
+    assert_close(np64(w.grad), dw64, 1e-4 * np.abs(dw64).max(), 1e-4, "w.grad")
 
 
 def test_add_rmsnorm_dy_only():
@@ -520,18 +530,53 @@ def test_rows_zero_and_errors():
         nr.rmsnorm(torch.ones(4, H), torch.ones(H), EPS)  # CPU tensors: no CPU path
 
 
-@pytest.mark.parametrize("T", [1, 4096])
-def test_config1_shape(T):
-    """Config 1 inputs (x [4, 512, 1536] fp16, w = 1 + 0.02 N, eps 1e-6; seeded) at T rows."""
+def _norm_case_vs_oracle(shape, g):
+    """rmsnorm fwd + bwd of x ~ N(0, 1) fp16 with w = 1 + 0.02 N(0, 1) (eps 1e-6) against the
+    fp64 oracle: y and dx at the 16-bit bar, dw within 1e-4 of max |dw|."""
     nr = _nr()
-    g = gen(0)
-    x = randn((T, H), g, dtype=torch.float16).requires_grad_()
+    x = randn(shape, g, dtype=torch.float16).requires_grad_()
     w = (1 + 0.02 * torch.randn(H, generator=g)).to(DEV).requires_grad_()
-    dy = randn((T, H), g, dtype=torch.float16)
+    dy = randn(shape, g, dtype=torch.float16)
     y = nr.rmsnorm(x, w, EPS)
     dx, dw = torch.autograd.grad(y, [x, w], dy)
-    y64, _ = ref.rmsnorm_fwd(np64(x), np64(w), EPS, "f16")
-    dx64, dw64 = ref.rmsnorm_bwd(np64(dy), np64(x), np64(w), EPS)
-    assert_close(np64(y), y64, 2e-3, 1e-2, "y")
-    assert_close(np64(dx), dx64, 2e-3, 1e-2, "dx")
+    assert y.shape == x.shape and dx.dtype == torch.float16
+    x2, dy2 = np64(x).reshape(-1, H), np64(dy).reshape(-1, H)
+    y64, _ = ref.rmsnorm_fwd(x2, np64(w), EPS, "f16")
+    dx64, dw64 = ref.rmsnorm_bwd(dy2, x2, np64(w), EPS)
+    assert_close(np64(y).reshape(-1, H), y64, 2e-3, 1e-2, "y")
+    assert_close(np64(dx).reshape(-1, H), dx64, 2e-3, 1e-2, "dx")
     assert_close(np64(dw), dw64, 1e-4 * np.abs(dw64).max(), 1e-4, "dw")
+
+
+def test_config1_shape():
+    """Config 1 at its own size: x [4, 512, 1536] fp16 (2048 rows), w = 1 + 0.02 N(0, 1),
+    eps 1e-6, seeded; y, dx and dw against the oracle."""
+    _norm_case_vs_oracle((4, 512, H), gen(0))
+
+
+def test_single_row():
+    """One row (the smallest input, a one-row grid)."""
+    _norm_case_vs_oracle((1, H), gen(1))
+
+
+def test_config3_norm_varlen_tokens():
+    """Config 3's norm half at its own size: the 8 sequences of lengths U[64, 1024] (seed 0)
+    packed to T = 4557 tokens, x [T, 1536] fp16."""
+    lens = torch.randint(64, 1025, (8,), generator=gen(0)).tolist()
+    assert lens == [113, 962, 544, 574, 556, 614, 422, 772] and sum(lens) == 4557
+    _norm_case_vs_oracle((sum(lens), H), gen(3))
+
+
+def test_one_row_views():
+    """A one-row input with a non-unit column stride, or an expanded row, is copied to
+    contiguous rows first (the kernels read unit-stride rows): the result equals the
+    contiguous input's bit for bit."""
+    nr = _nr()
+    g = gen(5)
+    base = randn((1, 2 * H), g, dtype=torch.bfloat16)
+    w = (1 + 0.02 * torch.randn(H, generator=g)).to(DEV)
+    strided = base[:, ::2]
+    assert torch.equal(nr.rmsnorm(strided, w, EPS), nr.rmsnorm(strided.contiguous(), w, EPS))
+    row = randn((H,), g, dtype=torch.bfloat16)
+    expanded = row.expand(3, H)
+    assert torch.equal(nr.rmsnorm(expanded, w, EPS), nr.rmsnorm(expanded.contiguous(), w, EPS))

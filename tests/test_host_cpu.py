@@ -85,3 +85,17 @@ def test_bench_byte_model_matches_baseline():
     assert round(norm / 1e6, 2) == 125.90 and round(rope / 1e6, 2) == 117.44
     total = (2 * c["layers"] + 1) * norm + c["layers"] * rope
     assert abs(total / 1e9 - 10.465) < 1e-3
+
+
+def test_rows_ld_rejects_strided_and_expanded_rows():
+    """A one-row view with a non-unit column stride, an expanded row and overlapping rows are
+    refused instead of read as if contiguous (the kernels take unit-stride, non-overlapping
+    rows)."""
+    n = 1536
+    assert _hip._rows_ld(torch.zeros(3, n), n) == n
+    assert _hip._rows_ld(torch.zeros(1, n), n) == n
+    assert _hip._rows_ld(torch.zeros(4, 2 * n)[:, :n], n) == 2 * n
+    for bad in (torch.zeros(1, 2 * n)[:, ::2], torch.zeros(1).expand(1, n),
+                torch.zeros(n).expand(4, n), torch.zeros(1, 1).expand(3, n)):
+        with pytest.raises(_hip.EsepError):
+            _hip._rows_ld(bad, n)
