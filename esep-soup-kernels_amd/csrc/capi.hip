@@ -46,13 +46,13 @@ void norm_shape(int64_t n, int* wpr, int* nv) {
   *nv = v < 2 ? 2 : v;
 }
 
-// Row groups per backward block with a weight gradient: blocks of up to 512 threads (one row
-// group of wpr wavefronts when a row needs more). Measured on MI355X against 1024-thread blocks
-// (config 4 / config 5 backward per launch): 512 threads 19.2 / 247 us (with the P below),
-// 1024 threads 19.7 / 255 us, 768 19.6 / 265, 256 22.3 / 422.
-constexpr int kBwdBlockThreads = 512;
+// Threads per backward block with a weight gradient: 256 when a row is one wavefront (n <= 1536:
+// four row groups, each lane summing its columns over 8 rows at config 4), else 512 (one or
+// more groups of wpr wavefronts). Measured at config 4 (8192 x 1536, main kernel with its
+// partials): 256 threads 15.6 us, 512 threads 16.0 us; P = 512 blocks of 256 threads 15.7 us.
+int bwd_block_threads(int wpr) { return wpr == 1 ? 256 : 512; }
 int bwd_groups(int wpr) {
-  const int g = kBwdBlockThreads / (64 * wpr);
+  const int g = bwd_block_threads(wpr) / (64 * wpr);
   return g > 0 ? g : 1;
 }
 
@@ -101,6 +101,11 @@ int attn_split(int64_t T, int HQ, int HK) {
 }
 
 }  // namespace
+
+namespace esep {
+hipError_t launch_stream_probe(const void* a, const void* b, void* out, int64_t bytes, int blocks,
+                               hipStream_t s);
+}
 
 extern "C" {
 
@@ -244,12 +249,10 @@ int esep_rmsnorm_bwd(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
   int wpr, nv;
   norm_shape(n, &wpr, &nv);
   a.wpr = wpr;
-  // Without a weight gradient every row group owns one row and small blocks (4 row groups of
-  // one wavefront, or one group of wpr wavefronts) let finished waves be replaced one by one.
+  // Without a weight gradient: blocks of 4 row groups of one wavefront (or one group of wpr
+  // wavefronts).
   const int gpb = part ? bwd_groups(wpr) : (wpr >= 4 ? 1 : 4 / wpr);
   a.gpb = gpb;
-  const int64_t blocks = part ? bwd_partials(rows, n) : (rows + gpb - 1) / gpb;
-  if (blocks > 0x7fffffff) return fail(ESEP_ESHAPE, "rmsnorm_bwd: too many rows");
 
   const int xdt = n_dy > 0 ? x_dt : ESEP_F32;
   const int dydt = n_dy > 0 ? dy_dt : xdt;
@@ -264,21 +267,36 @@ int esep_rmsnorm_bwd(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
   if (n_special > 0) vec = vec && aligned16(slot);
   a.vec = vec ? 1 : 0;
 
-  // LDS. The fast kernel (vector rows, one dy, xhat from x, no dr_out) stages the weight vector
-  // in one slot of nv * 64 * wpr * 8 floats and, with a weight gradient, keeps one accumulator
-  // slot per row group (at most (16 + 1) * 3 * 2 KiB per wpr: <= 144 KiB for n <= 16384). The
+  // The fast kernels (vector rows, one dy, xhat from x, no dr_out). Rows of one wavefront
+  // (n <= 1536) run the pipelined kernel, grid-strided: without a weight gradient on at most
+  // 512 blocks of 4 wavefronts (8 per CU; config 4: 4 rows each, 14.1 us against 15.4 us for
+  // one row per group over 2048 blocks). Wider rows run the wide kernel, one row per group.
+  const int threads = gpb * 64 * wpr;
+  const bool plain = vec && n_dy == 1 && !from_y && dr_out == nullptr && n_special == 0;
+  a.fast = 0;
+  if (plain && wpr == 1 && threads <= esep::kBwdPipeThreads && rows < (int64_t{1} << 30))
+    a.fast = 1;  // 32-bit row indices
+  else if (plain)
+    a.fast = 2;
+  int64_t blocks = part ? bwd_partials(rows, n) : (rows + gpb - 1) / gpb;
+  if (!part && a.fast == 1 && blocks > 512) blocks = 512;
+  if (blocks > 0x7fffffff) return fail(ESEP_ESHAPE, "rmsnorm_bwd: too many rows");
+  // LDS. The pipelined kernel keeps, with a weight gradient, one slot of nv * 64 * 8 floats per
+  // row group for the block sum (4 groups: 24 KiB). The wide kernel also stages the weight
+  // vector in one slot of nv * 64 * wpr * 8 floats (at most (8 + 1) * 3 * 2 KiB per wpr). The
   // general kernel parks at most bwd_tree_lds slots at once (it always runs NV = 3 element-wise).
-  const bool fast = vec && n_dy == 1 && !from_y && dr_out == nullptr && n_special == 0;
   const size_t slot_bytes = (size_t)nv * 64 * wpr * 8 * sizeof(float);
   size_t lds = 0;
-  if (fast)
+  if (a.fast == 1)
+    lds = part ? (size_t)gpb * slot_bytes : 0;
+  else if (a.fast == 2)
     lds = (part ? (size_t)gpb + 1 : 1) * slot_bytes;
   else if (part)
     lds = bwd_tree_lds(gpb, vec ? nv : 3, wpr);
   bool sup = false;
   hipStream_t s = static_cast<hipStream_t>(stream);
   hipError_t e = esep::launch_rmsnorm_bwd(a, xdt, dydt, odt, nv, dim3((unsigned)blocks),
-                                          dim3(gpb * 64 * wpr), lds, s, &sup);
+                                          dim3(threads), lds, s, &sup);
   if (!sup)
     return fail(ESEP_EINVAL, "rmsnorm_bwd: unsupported dtypes x=%d dy=%d dx=%d", xdt, dydt, odt);
   if (e != hipSuccess) return hip_fail(e, "rmsnorm_bwd launch");
@@ -687,6 +705,22 @@ int esep_head_row_softmax(void* z, int64_t ld, const int64_t* target, const floa
       esep::launch_head_row(a, dt, vec, static_cast<hipStream_t>(stream), &sup);
   if (!sup) return fail(ESEP_EINVAL, "head_row_softmax: unsupported dtype");
   return e == hipSuccess ? 0 : hip_fail(e, "head_row_softmax launch");
+}
+
+int esep_stream_probe(const void* a, const void* b, void* out, int64_t bytes, int blocks,
+                      void* stream) {
+  g_err[0] = 0;
+  if (a == nullptr || out == nullptr)
+    return fail(ESEP_EINVAL, "stream_probe: a and out are required");
+  if (!aligned16(a) || !aligned16(out) || (b != nullptr && !aligned16(b)))
+    return fail(ESEP_EALIGN, "stream_probe: buffers must be 16-byte aligned");
+  if (bytes < 0 || (bytes & 15) != 0 || blocks < 1 || blocks > (1 << 20))
+    return fail(ESEP_ESHAPE, "stream_probe: bytes=%lld must be a multiple of 16, blocks=%d in "
+                "[1, 2^20]", (long long)bytes, blocks);
+  if (bytes == 0) return 0;
+  const hipError_t e = esep::launch_stream_probe(a, b, out, bytes, blocks,
+                                                 static_cast<hipStream_t>(stream));
+  return e == hipSuccess ? 0 : hip_fail(e, "stream_probe launch");
 }
 
 }  // extern "C"

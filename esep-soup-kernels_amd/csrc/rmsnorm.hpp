@@ -71,6 +71,8 @@ struct BwdArgs {
   int wpr;
   int gpb;  // row groups per block (blockDim.x / (64 * wpr))
   int vec;
+  int fast;  // set by the entry point with the launch shape: 0 the general or API kernel,
+             // 1 the pipelined kernel (rows of one wavefront), 2 the wide fast kernel
 };
 
 constexpr int kFwdMaxThreads = 1024;
@@ -468,16 +470,185 @@ __device__ __forceinline__ void bwd_rows(const BwdArgs& a, float* red, float* ld
   if (want_dw) dw_block_partial<NV, VEC>(a, acc, lds, grp, gpb, tg, G);
 }
 
-// Fast backward for the common call: one gradient of y, xhat from x (not from y), no dr_out,
-// 16-byte-aligned whole chunks. LDS holds, per block, the weight vector (staged once, read by
-// every row instead of through L2: at n = 3584 that is 14 KiB per row) and, with a weight
-// gradient, one slot of NV * G * 8 floats per row group, indexed by column. Each lane keeps its
-// dy * xhat sums in registers over the rows of its group (the LDS of a weight-gradient block
-// already limits a CU to that one block, so the registers cost no occupancy), parks them in its
-// group's slot at the end, and the block sums the slots in group order. Each row's dy and x are
-// loaded at the top of its iteration: prefetching the next row into registers measured slower.
+// Fast backward for the common call (one gradient of y, xhat from x, not from y, no dr_out,
+// 16-byte-aligned whole chunks) on rows of one wavefront (n <= 1536). Rows are grid-strided (row group g of block b takes rows
+// (b + i * P) * gpb + g) and software-pipelined: two register sets with fixed roles hold the
+// raw (still packed) dy and x of two rows, and row i + 1's loads are issued before row i is
+// computed and stored. The sets alternate by loop unrolling, never by copying: a copy of a
+// prefetched register would wait for its load and serialize the rows again. Each lane always
+// owns the same columns, so its weight chunks (NV * 8 floats) are loaded once into registers
+// (no LDS staging, no barrier before the first row). With a weight gradient, each lane sums
+// dy * xhat of its chunks in registers over its group's rows; at the end the groups park their
+// sums in one LDS slot each (NV * G * 8 floats) and the block adds the slots in group order
+// into its row of the [P, n] partials.
 template <int NV, typename TX, typename TDY, typename TO>
-__device__ __forceinline__ void bwd_rows_fast(const BwdArgs& a, float* red, float* lds) {
+__device__ __forceinline__ void bwd_rows_pipe(const BwdArgs& a, float* lds) {
+  constexpr int G = kWave;  // one wavefront per row: every row reduction is a DPP wave sum
+  const int gpb = a.gpb;  // blockDim.x would cost a vector load of the hidden kernel arguments
+  const int grp = wave_id();
+  const int tg = (int)threadIdx.x & (kWave - 1);
+  const int lane = tg;
+  const int n = a.n;
+  // 32-bit scalar row indices (the entry point sends rows < 2^31 here): scalar compares, no
+  // 64-bit vector compare per row
+  const int rows = (int)a.rows;
+  const int step = (int)gridDim.x * gpb;  // grid-strided rows
+  const int first = (int)blockIdx.x * gpb + grp;
+  const int iters = (rows - first + step - 1) / step;  // rows of this group (block-uniform count)
+  const int iters_blk = (rows - (int)blockIdx.x * gpb + step - 1) / step;
+  const bool want_dw = a.part != nullptr;
+  const float inv_n = 1.0f / (float)n;
+
+  float wr[NV][8];  // chunks past the row read 0
+  {
+    const Span rw = make_span(a.w, (uint32_t)n * 4u);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) bload<true, float, kCached>(rw, (tg + k * G) * 32, wr[k]);
+  }
+  // Saved rstd of this group's rows it0 .. it0 + 63: lane l holds row first + (it0 + l) * step,
+  // read per row with readlane (one load per 64 rows, none in the row loop).
+  float rstd64 = 1.f;
+  auto load_rstd = [&](int it0) {
+    if (a.rstd != nullptr) {
+      const int it = it0 + lane;
+      rstd64 = it < iters ? a.rstd[first + (int64_t)it * step] : 1.f;
+    }
+  };
+  load_rstd(0);
+
+  Raw<TDY> rdy[2][NV];
+  Raw<TX> rx[2][NV];
+  // Loads of one row into register set `set`; a row past the end gets 0-byte buffers (its
+  // loads read 0 without touching memory).
+  auto fetch = [&](int set, int row) {
+    const bool ok = row < rows;
+    const Span sd = row_rsrc<TDY>(a.dy[0], row, a.ld_dy, n, ok);
+    const Span sx = row_rsrc<TX>(a.x, row, a.ld_x, n, ok);
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      rdy[set][k] = Buf<TDY>::template load_raw<kStream>(sd, (tg + k * G) * 8 * sizeof(TDY));
+      rx[set][k] = Buf<TX>::template load_raw<kStream>(sx, (tg + k * G) * 8 * sizeof(TX));
+    }
+  };
+
+  float dwa[NV][8];
+#pragma unroll
+  for (int k = 0; k < NV; ++k)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dwa[k][e] = 0.f;
+
+  // Row `it` of this group from register set `set`:
+  // dx = rstd * (g - xhat * mean(g * xhat)), g = dy * w.
+  auto finish = [&](int set, int it) {
+    const int row = first + it * step;
+    const bool ok = row < rows;  // a row that does not exist has dy = x = 0: adds nothing
+    float dy[NV][8], x[NV][8];
+#pragma unroll
+    for (int k = 0; k < NV; ++k) {
+      Buf<TDY>::unpack(rdy[set][k], dy[k]);
+      Buf<TX>::unpack(rx[set][k], x[k]);
+    }
+    float inv;
+    if (a.rstd != nullptr) {
+      inv = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(rstd64), it & (kWave - 1)));
+    } else {
+      float ss = 0.f;
+#pragma unroll
+      for (int k = 0; k < NV; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss = fmaf(x[k][e], x[k][e], ss);
+      inv = inv_rms(wave_sum(ss), n, a.eps);
+    }
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[k][e] *= inv;
+    if (want_dw) {
+#pragma unroll
+      for (int k = 0; k < NV; ++k)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dwa[k][e] = fmaf(dy[k][e], x[k][e], dwa[k][e]);
+    }
+    float p = 0.f;
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        dy[k][e] *= wr[k][e];
+        p = fmaf(dy[k][e], x[k][e], p);
+      }
+    const float proj = wave_sum(p) * inv_n;
+#pragma unroll
+    for (int k = 0; k < NV; ++k)
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dy[k][e] = inv * (dy[k][e] - x[k][e] * proj);
+    if (a.dr != nullptr) {
+      const Span so = row_rsrc<float>(a.dr, row, a.ld_out, n, ok);
+#pragma unroll
+      for (int k = 0; k < NV; ++k) bstore<true, float>(so, (tg + k * G) * 32, dy[k]);
+    }
+    if (a.dx != nullptr) {
+      const Span so = row_rsrc<TO>(a.dx, row, a.ld_out, n, ok);
+#pragma unroll
+      for (int k = 0; k < NV; ++k) bstore<true, TO>(so, (tg + k * G) * 8 * sizeof(TO), dy[k]);
+    }
+  };
+
+  // Two rows per pass with both register sets always consumed (an odd last row is peeled off
+  // after the loop): no path reaches the loop head with a set's loads still in flight, so the
+  // compiler's waits stay on the row being finished. The pass count is the block's (the
+  // groups of a block differ by at most one row; a group's surplus rows read 0 and store
+  // nothing).
+  fetch(0, first);
+  int it = 0;
+  for (; it + 2 <= iters_blk; it += 2) {
+    if (it != 0 && (it & (kWave - 1)) == 0) load_rstd(it);
+    fetch(1, first + (it + 1) * step);
+    finish(0, it);
+    fetch(0, first + (it + 2) * step);
+    finish(1, it + 1);
+  }
+  if (it < iters_blk) {
+    if (it != 0 && (it & (kWave - 1)) == 0) load_rstd(it);
+    finish(0, it);
+  }
+
+  if (want_dw) {
+    const int stride = NV * G * 8;  // floats per slot (>= n; the tail past n stays 0)
+    float* acc = lds + grp * stride;
+#pragma unroll
+    for (int k = 0; k < NV; ++k) Chunk<float>::store(acc + 8 * (tg + k * G), dwa[k]);
+    // block sum: column quads over all threads, groups added in group order
+    __syncthreads();
+    float* dst = a.part + (int64_t)blockIdx.x * n;
+    for (int q = threadIdx.x; 4 * q < n; q += gpb * G) {
+      f32x4 t = *reinterpret_cast<const f32x4*>(lds + 4 * q);
+      for (int g = 1; g < gpb; ++g) t += *reinterpret_cast<const f32x4*>(lds + g * stride + 4 * q);
+      *reinterpret_cast<f32x4*>(dst + 4 * q) = t;
+    }
+  }
+}
+
+// The pipelined backward's kernel: at most 512 threads, so each wavefront may hold up to 256
+// VGPRs (two register sets of raw rows, the weight chunks and the weight-gradient sums; 120 to
+// 220 with the element types) without spilling.
+constexpr int kBwdPipeThreads = 512;
+template <int NV, typename TX, typename TDY, typename TO>
+__global__ __launch_bounds__(kBwdPipeThreads) void k_rmsnorm_bwd_pipe(const BwdArgs a) {
+  extern __shared__ float lds[];
+  bwd_rows_pipe<NV, TX, TDY, TO>(a, lds);
+}
+
+// Fast backward for rows of several wavefronts (n > 1536): the same call pattern as
+// bwd_rows_pipe. LDS holds, per block, the weight vector (staged once, read by every row instead
+// of through L2: at n = 3584 that is 14 KiB per row) and, with a weight gradient, one slot of
+// NV * G * 8 floats per row group, indexed by column. Each lane keeps its dy * xhat sums in
+// registers over the rows of its group, parks them in its group's slot at the end, and the
+// block sums the slots in group order. Each row's dy and x are loaded at the top of its
+// iteration: at n = 3584 (three wavefronts per row, a barrier in every row reduction) the
+// pipelined form measured slower (config 5 backward 242 -> 262 us).
+template <int NV, typename TX, typename TDY, typename TO>
+__device__ __forceinline__ void bwd_rows_wide(const BwdArgs& a, float* red, float* lds) {
   const int G = kWave * a.wpr;
   const int gpb = a.gpb;  // blockDim.x would cost a vector load of the hidden kernel arguments
   const int grp = wave_id() / a.wpr;
@@ -583,6 +754,13 @@ __device__ __forceinline__ void bwd_rows_fast(const BwdArgs& a, float* red, floa
   }
 }
 
+template <int NV, typename TX, typename TDY, typename TO>
+__global__ __launch_bounds__(kBwdThreads) void k_rmsnorm_bwd_wide(const BwdArgs a) {
+  __shared__ float red[kBwdThreads / kWave];
+  extern __shared__ float lds[];
+  bwd_rows_wide<NV, TX, TDY, TO>(a, red, lds);
+}
+
 // Backward of the reference API's calls without a weight gradient or exact channels (up to 5
 // gradients of y, dr_out, xhat from x or from y = w * xhat) in blocks of at most 256 threads:
 // every load of a row (all dys, x, dr_out) is issued before any is used. The general kernel
@@ -681,15 +859,12 @@ __global__ __launch_bounds__(kBwdApiThreads) void k_rmsnorm_bwd_api(const BwdArg
   }
 }
 
-// FAST: bwd_rows_fast (only with VEC); else the general bwd_rows.
-template <int NV, bool VEC, bool FAST, typename TX, typename TDY, typename TO>
+// The general backward (every reference mode; vector or element-wise rows).
+template <int NV, bool VEC, typename TX, typename TDY, typename TO>
 __global__ __launch_bounds__(kBwdThreads) void k_rmsnorm_bwd(const BwdArgs a) {
   __shared__ float red[kBwdThreads / kWave];
   extern __shared__ float lds[];
-  if constexpr (FAST)
-    bwd_rows_fast<NV, TX, TDY, TO>(a, red, lds);
-  else
-    bwd_rows<NV, VEC, TX, TDY, TO>(a, red, lds);
+  bwd_rows<NV, VEC, TX, TDY, TO>(a, red, lds);
 }
 
 // Stage 2 of the weight gradient: dw[j] = sum_p part[p, j]. A block of 256 threads owns

@@ -12,11 +12,24 @@ template <typename TX, typename TDY, typename TO>
 static hipError_t bwd_nv(const BwdArgs& a, int nv, dim3 grid, dim3 block, size_t lds,
                          hipStream_t s) {
   if (!a.vec) {
-    hipLaunchKernelGGL((k_rmsnorm_bwd<3, false, false, TX, TDY, TO>), grid, block, lds, s, a);
+    hipLaunchKernelGGL((k_rmsnorm_bwd<3, false, TX, TDY, TO>), grid, block, lds, s, a);
     return hipGetLastError();
   }
-  // The fast kernel serves the plain backward: one dy, xhat from x, no dr_out.
-  const bool fast = a.n_dy == 1 && !a.from_y && a.dr_out == nullptr && a.n_special == 0;
+  // The fast kernels serve the plain backward (one dy, xhat from x, no dr_out): the pipelined
+  // one for rows of one wavefront, the wide one otherwise; the entry point decides with the
+  // launch shape.
+  const bool fast = a.fast != 0;
+  if (a.fast == 1) {
+    if (block.x > (unsigned)kBwdPipeThreads || a.wpr != 1) return hipErrorInvalidValue;
+    if (nv == 2) hipLaunchKernelGGL((k_rmsnorm_bwd_pipe<2, TX, TDY, TO>), grid, block, lds, s, a);
+    else hipLaunchKernelGGL((k_rmsnorm_bwd_pipe<3, TX, TDY, TO>), grid, block, lds, s, a);
+    return hipGetLastError();
+  }
+  if (a.fast == 2) {
+    if (nv == 2) hipLaunchKernelGGL((k_rmsnorm_bwd_wide<2, TX, TDY, TO>), grid, block, lds, s, a);
+    else hipLaunchKernelGGL((k_rmsnorm_bwd_wide<3, TX, TDY, TO>), grid, block, lds, s, a);
+    return hipGetLastError();
+  }
   // The reference API's other calls without a weight gradient or exact channels.
   if (!fast && a.part == nullptr && a.n_special == 0 && a.n_dy > 0 &&
       block.x <= (unsigned)kBwdApiThreads) {
@@ -24,13 +37,8 @@ static hipError_t bwd_nv(const BwdArgs& a, int nv, dim3 grid, dim3 block, size_t
     else hipLaunchKernelGGL((k_rmsnorm_bwd_api<3, TX, TDY, TO>), grid, block, 0, s, a);
     return hipGetLastError();
   }
-  switch (nv * 2 + (fast ? 1 : 0)) {
-    case 4: hipLaunchKernelGGL((k_rmsnorm_bwd<2, true, false, TX, TDY, TO>), grid, block, lds, s, a); break;
-    case 5: hipLaunchKernelGGL((k_rmsnorm_bwd<2, true, true, TX, TDY, TO>), grid, block, lds, s, a); break;
-    case 6: hipLaunchKernelGGL((k_rmsnorm_bwd<3, true, false, TX, TDY, TO>), grid, block, lds, s, a); break;
-    case 7: hipLaunchKernelGGL((k_rmsnorm_bwd<3, true, true, TX, TDY, TO>), grid, block, lds, s, a); break;
-    default: return hipErrorInvalidValue;
-  }
+  if (nv == 2) hipLaunchKernelGGL((k_rmsnorm_bwd<2, true, TX, TDY, TO>), grid, block, lds, s, a);
+  else hipLaunchKernelGGL((k_rmsnorm_bwd<3, true, TX, TDY, TO>), grid, block, lds, s, a);
   return hipGetLastError();
 }
 

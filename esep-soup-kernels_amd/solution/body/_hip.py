@@ -57,6 +57,7 @@ SIGNATURES = {
     "esep_attn_bwd": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp,
                              _vp, _i64, _vp, _i64, _vp, _i64, _i32, _i64, _i32, _i32, _i32, _vp,
                              _i32, _i32, _f32, _vp]),
+    "esep_stream_probe": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp]),
     "esep_rope": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64,
                          _i32, _i32, _i32, _vp, _i32, _vp, _vp, _i32, _vp, _f32, _vp]),
 }
@@ -247,7 +248,7 @@ def rmsnorm_bwd(dys, x, w, eps, from_y=False, rstd=None, dr_out=None, slot=None,
     _record(name)
 
 
-def dgamma_reduce(partials, dw):
+def dgamma_reduce(partials, dw, name="_dgamma_reduce"):
     """dw[j] = sum_p partials[p, j] (fp32 [P, n] contiguous) in the fixed order of
     esep_dgamma_reduce; dw: [n] fp32 / fp16 / bf16 out."""
     dev = _dev(partials, dw)
@@ -259,6 +260,7 @@ def dgamma_reduce(partials, dw):
     rc = lib().esep_dgamma_reduce(_p(partials) if P else None, P, n, _p(dw), dtype_code(dw.dtype),
                                   _stream(dev))
     _check(rc, "esep_dgamma_reduce")
+    _record(name)
 
 
 class DgammaItem(ctypes.Structure):
@@ -269,7 +271,7 @@ class DgammaItem(ctypes.Structure):
 DGAMMA_BATCH_MAX = 64
 
 
-def dgamma_reduce_batch(partials, dws):
+def dgamma_reduce_batch(partials, dws, name="_dgamma_reduce_batch"):
     """Stage 2 of several norms in one launch (esep_dgamma_reduce_batch): dws[i] gets exactly
     what dgamma_reduce(partials[i], dws[i]) would write. partials: fp32 [P_i, n] contiguous
     tensors (P_i may differ), dws: contiguous [n] tensors of one float dtype."""
@@ -287,6 +289,7 @@ def dgamma_reduce_batch(partials, dws):
     rc = lib().esep_dgamma_reduce_batch(ctypes.cast(arr, _vp), len(dws), n, dtype_code(dws[0].dtype),
                                         _stream(dev))
     _check(rc, "esep_dgamma_reduce_batch")
+    _record(name)
 
 
 def rope(q, k, qo, ko, inv_freq, sign, q_delta=None, positions=None, cu_seqlens=None,
@@ -546,4 +549,19 @@ def head_row_softmax(z, target, cew, lse, tlogit, ent, amax, write_g, g_scale,
                                      _p(amax), rows, V, 1 if write_g else 0, float(g_scale),
                                      dtype_code(z.dtype), _stream(dev))
     _check(rc, "esep_head_row_softmax")
+    _record(name)
+
+
+def stream_probe(a, out, b=None, blocks=1024, name="_stream_probe"):
+    """out = a (+ b) over the bytes of out (esep_stream_probe): the streaming ceiling bench.py
+    compares the path kernels with. Contiguous tensors of out's byte size."""
+    dev = _dev(a, b, out)
+    nbytes = out.numel() * out.element_size()
+    for t in (a, b):
+        if t is not None and (not t.is_contiguous() or t.numel() * t.element_size() != nbytes):
+            raise EsepError("stream_probe inputs must be contiguous and as large as out")
+    if not out.is_contiguous():
+        raise EsepError("stream_probe out must be contiguous")
+    rc = lib().esep_stream_probe(_p(a), _p(b), _p(out), nbytes, int(blocks), _stream(dev))
+    _check(rc, "esep_stream_probe")
     _record(name)

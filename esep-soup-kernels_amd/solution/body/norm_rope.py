@@ -35,6 +35,7 @@ rmsnorm(x, weight, eps, out_dtype=None, recompute_rstd=False) -> y
 """
 
 import math
+import threading
 
 import torch
 
@@ -103,6 +104,107 @@ def _rows_of(t, dtype=None):
     return flat.contiguous()
 
 
+# ----------------------------------------------------------------------------------------
+# Weight gradient: stage 2 deferred to the end of the backward pass
+# ----------------------------------------------------------------------------------------
+# A trainable norm weight's gradient is reduced in two fixed-order stages: the backward kernel
+# writes [P, n] fp32 partials (P depends on the shape only) and stage 2 sums them over P. With
+# DEFER_WEIGHT_GRAD on (read at call time), a backward pass that accumulates into the weight's
+# .grad (loss.backward(), not autograd.grad) keeps each norm's partials and runs stage 2 once
+# at the end of the pass for every norm (esep_dgamma_reduce_batch: one launch per 64 norms
+# instead of one per norm), then accumulates the results into .grad. The gradients are the same
+# bits either way. It is not used (each backward reduces its own partials and returns dw as
+# usual) under autograd.grad or backward(inputs=...) without the weight, with hooks on the
+# weight, for a double backward (create_graph=True), or inside a torch.distributed job (whose
+# gradient hooks expect every gradient through autograd).
+DEFER_WEIGHT_GRAD = True
+
+_defer_lock = threading.Lock()
+_deferred = {}  # autograd graph task id -> [(weight leaf, partials, stream)]
+
+
+def _weight_leaf(w):
+    """The leaf parameter a kernel weight comes from: w itself, or the leaf behind the
+    single-input casts of _weight_f32 (None when there is no such leaf)."""
+    if w.is_leaf:
+        return w if w.requires_grad else None
+    node = w.grad_fn
+    while node is not None and type(node).__name__ != "AccumulateGrad":
+        nxt = [f for f, _ in node.next_functions if f is not None]
+        if len(nxt) != 1:
+            return None
+        node = nxt[0]
+    return getattr(node, "variable", None)
+
+
+def _can_defer(leaf):
+    if not DEFER_WEIGHT_GRAD or leaf is None or not leaf.requires_grad or torch.is_grad_enabled():
+        return False
+    if leaf._backward_hooks or getattr(leaf, "_post_accumulate_grad_hooks", None):
+        return False
+    if torch.distributed.is_available() and torch.distributed.is_initialized():
+        return False
+    try:
+        node = torch.autograd.graph.get_gradient_edge(leaf).node
+        return bool(torch._C._will_engine_execute_node(node))
+    except RuntimeError:
+        return False
+
+
+def _defer(leaf, partials):
+    """Keep one norm's partials for the end of the current backward pass."""
+    task = torch._C._current_graph_task_id()
+    stream = torch.cuda.current_stream(partials.device)
+    with _defer_lock:
+        first = task not in _deferred
+        _deferred.setdefault(task, []).append((leaf, partials, stream))
+    if first:
+        torch.autograd.Variable._execution_engine.queue_callback(lambda: _finish_deferred(task))
+
+
+def _finish_deferred(task):
+    """End of a backward pass: stage 2 of every deferred norm, batched per (device, dtype, n),
+    accumulated into the weights' .grad on the caller's current stream (the engine has made it
+    wait for the leaf streams; the streams the partials were written on are waited for too)."""
+    with _defer_lock:
+        items = _deferred.pop(task, [])
+    groups = {}
+    for leaf, part, stream in items:
+        key = (part.device, leaf.dtype, part.shape[1])
+        groups.setdefault(key, []).append((leaf, part, stream))
+    with torch.no_grad():
+        for (dev, dtype, n), grp in groups.items():
+            cur = torch.cuda.current_stream(dev)
+            for st in {st for _, _, st in grp}:
+                if st != cur:
+                    cur.wait_stream(st)
+            out_dtype = dtype if dtype in _FLOATS else torch.float32
+            for i in range(0, len(grp), _hip.DGAMMA_BATCH_MAX):
+                chunk = grp[i:i + _hip.DGAMMA_BATCH_MAX]
+                dws = [torch.empty((n,), device=dev, dtype=out_dtype) for _ in chunk]
+                _hip.dgamma_reduce_batch([part for _, part, _ in chunk], dws)
+                for (leaf, part, _), dw in zip(chunk, dws):
+                    part.record_stream(cur)
+                    g = dw if dw.dtype == leaf.dtype else dw.to(leaf.dtype)
+                    if leaf.grad is None:
+                        leaf.grad = g
+                    else:
+                        leaf.grad.add_(g)
+
+
+def _weight_grad_target(ctx, w, rows, w_index):
+    """(dw buffer or None, partials or None) for a backward: partials when stage 2 is deferred
+    (dw is then not returned: it reaches .grad at the end of the pass), else a dw buffer when
+    the weight (apply() argument w_index) needs a gradient."""
+    if not ctx.needs_input_grad[w_index]:
+        return None, None
+    n = w.shape[0]
+    if rows > 0 and _can_defer(ctx.weight_leaf):
+        P = _hip.rmsnorm_partials(rows, n)
+        return None, torch.empty((P, n), device=w.device, dtype=torch.float32)
+    return torch.empty((n,), device=w.device, dtype=torch.float32), None
+
+
 class AddRMSNorm(torch.autograd.Function):
     """Reference: norm_rope.py:208-286 (same apply() arguments and saved tensors).
 
@@ -136,6 +238,7 @@ class AddRMSNorm(torch.autograd.Function):
                              slot=slots if k_exact else None, xs=xs, n_special=k_exact)
 
         ctx.save_for_backward(*((y, rstd, w, slots, xs) if save_y else (resid_out, rstd, w)))
+        ctx.weight_leaf = _weight_leaf(w) if w.requires_grad else None
         ctx.from_y, ctx.n_special, ctx.eps, ctx.shape = save_y, k_exact, eps, shape
         ctx.has_delta = add is not None
         ctx.delta_dtype = None if delta is None else delta.dtype
@@ -163,12 +266,14 @@ class AddRMSNorm(torch.autograd.Function):
         dev = x.device
         dr = torch.empty((rows, n), device=dev, dtype=torch.float32) if want_r else None
         ddelta = torch.empty((rows, n), device=dev, dtype=ctx.delta_dtype) if write_dd else None
-        dw = torch.empty((n,), device=dev, dtype=torch.float32) if want_w else None
+        dw, partials = _weight_grad_target(ctx, w, rows, 2)
         dr2 = dr_out.reshape(-1, n).to(torch.float32).contiguous() if has_dr else None
-        if rows > 0 and (dr is not None or ddelta is not None or dw is not None):
+        if rows > 0 and (dr is not None or ddelta is not None or want_w):
             _hip.rmsnorm_bwd(dys, x, w, ctx.eps, from_y=ctx.from_y, rstd=rstd, dr_out=dr2,
                              slot=slots if ctx.n_special else None, xs=xs,
-                             n_special=ctx.n_special, dr=dr, dx=ddelta, dw=dw)
+                             n_special=ctx.n_special, dr=dr, dx=ddelta, dw=dw, partials=partials)
+            if partials is not None:
+                _defer(ctx.weight_leaf, partials)
         elif dw is not None:
             dw.zero_()
         d_rin = dr.view(ctx.shape) if want_r else None
@@ -239,6 +344,7 @@ class RMSNorm(torch.autograd.Function):
         else:
             ctx.save_for_backward(x2, w, rstd)
         ctx.eps, ctx.shape, ctx.recompute = eps, shape, recompute_rstd
+        ctx.weight_leaf = _weight_leaf(w) if w.requires_grad else None
         return y.view(shape)
 
     @staticmethod
@@ -250,13 +356,13 @@ class RMSNorm(torch.autograd.Function):
         rows, n = x2.shape
         want_x, want_w = ctx.needs_input_grad[0], ctx.needs_input_grad[1]
         dx = torch.empty((rows, n), device=x2.device, dtype=x2.dtype) if want_x else None
-        dw = torch.empty((n,), device=x2.device, dtype=torch.float32) if want_w else None
+        dw, partials = _weight_grad_target(ctx, w, rows, 1)
         if rows > 0 and (want_x or want_w):
             dy2 = dy.reshape(-1, n).contiguous()
-            if x2.dtype == torch.float32:
-                _hip.rmsnorm_bwd([dy2], x2, w, ctx.eps, rstd=rstd, dr=dx, dw=dw)
-            else:
-                _hip.rmsnorm_bwd([dy2], x2, w, ctx.eps, rstd=rstd, dx=dx, dw=dw)
+            out = dict(dr=dx) if x2.dtype == torch.float32 else dict(dx=dx)
+            _hip.rmsnorm_bwd([dy2], x2, w, ctx.eps, rstd=rstd, dw=dw, partials=partials, **out)
+            if partials is not None:
+                _defer(ctx.weight_leaf, partials)
         elif dw is not None:
             dw.zero_()
         return (dx.view(ctx.shape) if want_x else None), dw, None, None, None

@@ -1,0 +1,187 @@
+"""The deferred weight-gradient stage 2 (norm_rope.DEFER_WEIGHT_GRAD): a loss.backward() pass
+keeps every trainable norm's [P, n] partials and reduces all of them in one
+esep_dgamma_reduce_batch launch at the end of the pass, then accumulates into .grad. The
+gradients must be the bits of the per-call reduction (the batched reduce sums each norm's
+partials in the same order), and every case where deferral cannot see the gradient's consumer
+(autograd.grad, backward(inputs=...), hooks, create_graph) must take the per-call path.
+
+Also: the streaming measurement kernel (esep_stream_probe) computes out = a (+ b)."""
+
+import numpy as np
+import pytest
+import torch
+
+from _util import DEV, assert_close, gen, np64, randn
+from oracle import norm_rope_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+H, EPS = 1536, 1e-6
+
+
+def _nr():
+    from solution.body import norm_rope
+
+    return norm_rope
+
+
+def _stack(seed, T=300, bf16_weight=False):
+    """Three norms in a chain (plain bf16 norm, residual-add norm, final norm) with trainable
+    weights, like a decoder layer's input / post-attention / final norms."""
+    g = gen(seed)
+    wdt = torch.bfloat16 if bf16_weight else torch.float32
+    ws = [torch.nn.Parameter((1 + 0.02 * torch.randn(H, generator=g)).to(wdt).to(DEV))
+          for _ in range(3)]
+    x = randn((T, H), g, dtype=torch.bfloat16).requires_grad_()
+    r = randn((T, H), g, 2.0).requires_grad_()
+    gy = [randn((T, H), g, dtype=dt) for dt in (torch.bfloat16, torch.bfloat16, torch.float32)]
+    return ws, x, r, gy
+
+
+def _run(ws, x, r, gy, defer, backward=None):
+    nr = _nr()
+    old = nr.DEFER_WEIGHT_GRAD
+    nr.DEFER_WEIGHT_GRAD = defer
+    try:
+        y0 = nr.rmsnorm(x, ws[0], EPS)
+        r1, y1 = nr.add_rmsnorm(r, y0, ws[1], EPS, torch.bfloat16)
+        _, y2 = nr.add_rmsnorm(r1, y1, ws[2], EPS, torch.float32)
+        loss = (y0.float() * gy[0].float()).sum() + (y1.float() * gy[1].float()).sum() \
+            + (y2 * gy[2]).sum()
+        if backward is None:
+            loss.backward()
+        else:
+            return backward(loss)
+    finally:
+        nr.DEFER_WEIGHT_GRAD = old
+
+
+@pytest.mark.parametrize("bf16_weight", [False, True], ids=["fp32_weight", "bf16_weight"])
+def test_deferred_equals_per_call_bitwise(bf16_weight):
+    from solution.body import _hip
+
+    ws_a, x, r, gy = _stack(1, bf16_weight=bf16_weight)
+    ws_b = [torch.nn.Parameter(w.detach().clone()) for w in ws_a]
+    xa, ra = x.detach().clone().requires_grad_(), r.detach().clone().requires_grad_()
+    with _hip.count_launches() as names:
+        _run(ws_a, xa, ra, gy, defer=True)
+        torch.cuda.synchronize()
+    assert names.count("_dgamma_reduce_batch") == 1 and names.count("_add_rmsnorm_bwd") == 3
+    xb, rb = x.detach().clone().requires_grad_(), r.detach().clone().requires_grad_()
+    with _hip.count_launches() as names_b:
+        _run(ws_b, xb, rb, gy, defer=False)
+        torch.cuda.synchronize()
+    assert names_b.count("_dgamma_reduce_batch") == 0
+    for wa, wb in zip(ws_a, ws_b):
+        assert wa.grad is not None and wa.grad.dtype == wa.dtype
+        assert torch.equal(wa.grad, wb.grad)
+    assert torch.equal(xa.grad, xb.grad) and torch.equal(ra.grad, rb.grad)
+
+
+def test_deferred_matches_oracle():
+    """The first norm's weight gradient against the fp64 closed form sum_t dy_tj * xhat_tj."""
+    ws, x, r, gy = _stack(2)
+    nr = _nr()
+    old = nr.DEFER_WEIGHT_GRAD
+    nr.DEFER_WEIGHT_GRAD = True
+    try:
+        y0 = nr.rmsnorm(x, ws[0], EPS)
+        (y0.float() * gy[0].float()).sum().backward()
+    finally:
+        nr.DEFER_WEIGHT_GRAD = old
+    _, dw64 = ref.rmsnorm_bwd(np64(gy[0]), np64(x), np64(ws[0]), EPS)
+    assert_close(np64(ws[0].grad), dw64, 1e-5 * np.abs(dw64).max(), 1e-5, "dw")
+
+
+def test_deferred_accumulates_over_passes():
+    """Two backward passes (gradient accumulation) give the per-call path's .grad."""
+    ws_a, x, r, gy = _stack(3)
+    ws_b = [torch.nn.Parameter(w.detach().clone()) for w in ws_a]
+    for _ in range(2):
+        _run(ws_a, x.detach().requires_grad_(), r.detach().requires_grad_(), gy, defer=True)
+        _run(ws_b, x.detach().requires_grad_(), r.detach().requires_grad_(), gy, defer=False)
+    for wa, wb in zip(ws_a, ws_b):
+        assert torch.equal(wa.grad, wb.grad)
+
+
+def test_not_deferred_when_the_engine_does_not_accumulate():
+    """autograd.grad and backward(inputs=...) without the weight: the per-call path (the weight
+    gradient is returned, or not computed into .grad at all)."""
+    from solution.body import _hip
+
+    ws, x, r, gy = _stack(4)
+    ref_ws = [torch.nn.Parameter(w.detach().clone()) for w in ws]
+    _run(ref_ws, x.detach().requires_grad_(), r.detach().requires_grad_(), gy, defer=False)
+    with _hip.count_launches() as names:
+        grads = _run(ws, x, r, gy, defer=True,
+                     backward=lambda loss: torch.autograd.grad(loss, ws))
+    assert names.count("_dgamma_reduce_batch") == 0
+    for gw, wb in zip(grads, ref_ws):
+        assert torch.equal(gw, wb.grad)
+    assert all(w.grad is None for w in ws)
+    _run(ws, x, r, gy, defer=True, backward=lambda loss: loss.backward(inputs=[x]))
+    torch.cuda.synchronize()
+    assert all(w.grad is None for w in ws) and x.grad is not None
+
+
+def test_not_deferred_with_hooks():
+    """A hook on the weight sees its gradient through autograd (no deferral for that weight)."""
+    ws, x, r, gy = _stack(5)
+    ref_ws = [torch.nn.Parameter(w.detach().clone()) for w in ws]
+    _run(ref_ws, x.detach().requires_grad_(), r.detach().requires_grad_(), gy, defer=False)
+    seen = {}
+    ws[1].register_hook(lambda g: seen.setdefault("grad", g.clone()))
+    _run(ws, x, r, gy, defer=True)
+    assert torch.equal(seen["grad"], ref_ws[1].grad)
+    for wa, wb in zip(ws, ref_ws):
+        assert torch.equal(wa.grad, wb.grad)
+
+
+def test_deferred_inside_graph_capture_replays():
+    """A whole forward + backward captured in a HIP graph with deferral on: every replay
+    rewrites the same .grad bits as the eager pass."""
+    nr = _nr()
+    g = gen(6)
+    w = torch.nn.Parameter((1 + 0.02 * torch.randn(H, generator=g)).to(DEV))
+    x = randn((512, H), g, dtype=torch.bfloat16).requires_grad_()
+    gy = randn((512, H), g, dtype=torch.bfloat16)
+
+    def step():
+        w.grad = None
+        y = nr.rmsnorm(x, w, EPS)
+        (y.float() * gy.float()).sum().backward()
+
+    step()
+    torch.cuda.synchronize()
+    eager = w.grad.clone()
+    s = torch.cuda.Stream()
+    s.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(s):
+        step()
+    torch.cuda.current_stream().wait_stream(s)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    w.grad = None
+    with torch.cuda.graph(graph):
+        y = nr.rmsnorm(x, w, EPS)
+        (y.float() * gy.float()).sum().backward()
+    captured = w.grad
+    for _ in range(3):
+        captured.fill_(float("nan"))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(captured, eager)
+
+
+@pytest.mark.parametrize("two", [False, True])
+def test_stream_probe_values(two):
+    from solution.body import _hip
+
+    g = torch.Generator(device=DEV).manual_seed(7)
+    a = torch.randint(0, 1 << 30, (1 << 20,), generator=g, device=DEV, dtype=torch.int32)
+    b = torch.randint(0, 1 << 30, (1 << 20,), generator=g, device=DEV, dtype=torch.int32) if two else None
+    out = torch.empty_like(a)
+    _hip.stream_probe(a, out, b, blocks=300)
+    want = a + b if two else a
+    assert torch.equal(out, want)
