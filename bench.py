@@ -10,15 +10,22 @@ Every layer owns its own tensors (as in training), ~9 GB resident in HBM before 
 The step is captured once in a HIP graph (the launches go through the C ABI of
 libesep_body.so, ordered on one stream) and replayed.
 
+The norm-weight gradients follow the Python API's schedule in a loss.backward() pass
+(norm_rope.DEFER_WEIGHT_GRAD): every norm backward writes its fixed-order partials and one
+batched launch after the sweep reduces all 57 (the per-call schedule, a reduce launch inside
+every norm backward, is timed too: config4_per_call_dgamma).
+
 value = algorithmic bytes of one step / measured seconds per step. Algorithmic bytes count
 each required tensor once (e = 2 bytes):
   RMSNorm fwd 2eTH + 4T (rstd)   RMSNorm bwd 3eTH + 4T (rstd) + 4H (dw)   RoPE 2eT(HQ+HK)D
 With --rstd recomputed the 4T terms go away (rstd is recomputed from x in backward).
 
 Also printed: the roofline of the dominant kernel (per-launch HIP-event timing of graphs of
-that kernel alone, on the stream it runs on) and the CPU baseline: the PyTorch-eager fp32
-restatement of HF's Qwen2RMSNorm / rotary path (oracle/hf_eager.py) timed on this host's
-cores on one layer of the same workload.
+that kernel alone, on the stream it runs on); the streaming ceiling (esep_stream_probe at each
+kernel's bytes and launch pattern, and the step those launches would take); configs 1-3
+(cache-resident and with the Infinity Cache flushed); config 5; the neighbours' kernels; and
+the CPU baseline: the PyTorch-eager fp32 restatement of HF's Qwen2RMSNorm / rotary path
+(oracle/hf_eager.py) timed on this host's cores on one layer of the same workload.
 
     python bench.py [--steps K] [--warmup W] [--rstd saved|recomputed] [--no-cpu]
 """
@@ -62,13 +69,13 @@ def rope_bytes(T, HQ, HK, D, e):
 class Body:
     """Resident tensors of the whole sweep and the launch sequence of one step."""
 
-    def __init__(self, cfg, save_rstd, dev, batched_dgamma=False):
+    def __init__(self, cfg, save_rstd, dev, deferred_dgamma=True):
         import torch
 
         from solution.body import _hip
 
         self.hip, self.cfg, self.save_rstd = _hip, cfg, save_rstd
-        self.batched_dgamma = batched_dgamma
+        self.deferred = deferred_dgamma
         L, B, S, H, HQ, HK, D = (cfg[k] for k in ("layers", "B", "S", "H", "HQ", "HK", "D"))
         T = B * S
         self.T = T
@@ -90,10 +97,11 @@ class Body:
         self.dx = [torch.empty(T, H, device=dev, dtype=bf) for _ in range(n_norms)]
         self.dw = [torch.empty(H, device=dev) for _ in range(n_norms)]
         self.ws = torch.empty(max(_hip.rmsnorm_partials(T, H), 1), H, device=dev)
-        # batched stage 2: every norm backward of the sweep keeps its own partials, and one
-        # launch after the sweep reduces all of them (esep_dgamma_reduce_batch)
+        # deferred stage 2 (the Python API's schedule in a loss.backward() pass,
+        # norm_rope.DEFER_WEIGHT_GRAD): every norm backward of the sweep keeps its own partials
+        # and one launch after the sweep reduces all of them (esep_dgamma_reduce_batch)
         self.parts = ([torch.empty(_hip.rmsnorm_partials(T, H), H, device=dev) for _ in range(n_norms)]
-                      if batched_dgamma else None)
+                      if deferred_dgamma else None)
         self.q = [rn(B, S, HQ, D) for _ in range(L)]
         self.k = [rn(B, S, HK, D) for _ in range(L)]
         self.qo = [torch.empty_like(t) for t in self.q]
@@ -109,7 +117,7 @@ class Body:
         self.hip.rmsnorm_fwd(self.x[i], self.w[i], self.y[i], self.cfg["eps"], rstd=self.rstd[i])
 
     def norm_bwd(self, i):
-        if self.batched_dgamma:
+        if self.deferred:
             self.hip.rmsnorm_bwd([self.dy[i]], self.x[i], self.w[i], self.cfg["eps"],
                                  rstd=self.rstd[i], dx=self.dx[i], partials=self.parts[i])
             return
@@ -136,8 +144,11 @@ class Body:
             self.norm_bwd(2 * l + 1)
             self.rope_bwd(l)
             self.norm_bwd(2 * l)
-        if self.batched_dgamma:
-            self.hip.dgamma_reduce_batch(self.parts, self.dw)
+        if self.deferred:
+            self.dgamma_stage2()
+
+    def dgamma_stage2(self):
+        self.hip.dgamma_reduce_batch(self.parts, self.dw)
 
     def step_bytes(self):
         c, T, e = self.cfg, self.T, 2
@@ -252,13 +263,13 @@ def run_config5(dev, steps):
             "kernels": kernels}
 
 
-def run_config4_batched_dgamma(dev, steps, save_rstd):
-    """Config 4's step with the weight-gradient stage 2 batched: the 57 norm backwards of the sweep
-    write their own partials and one esep_dgamma_reduce_batch launch after the sweep sums all of
-    them (the same bits as one reduce per norm). Same bytes; 56 launches fewer per step."""
+def run_config4_per_call_dgamma(dev, steps, save_rstd):
+    """Config 4's step with the weight-gradient stage 2 inside every norm backward call (what a
+    backward pass gets that cannot defer it: autograd.grad, hooks on the weight, create_graph):
+    one reduce launch per norm. Same bytes; 56 launches more per step."""
     import torch
 
-    body = Body(CFG4, save_rstd, dev, batched_dgamma=True)
+    body = Body(CFG4, save_rstd, dev, deferred_dgamma=False)
     torch.cuda.synchronize()
     g = capture(body.step)
     time_graph(g, 2)
@@ -266,13 +277,179 @@ def run_config4_batched_dgamma(dev, steps, save_rstd):
     ms = max(ev_ms, wall_ms)
     nbytes = body.step_bytes()
     gbs = nbytes / (ms * 1e-3) / 1e9
-    log(f"config 4, batched weight-gradient stage 2: {ms:.3f} ms per step, {gbs:.0f} GB/s = "
+    log(f"config 4, weight-gradient stage 2 per call: {ms:.3f} ms per step, {gbs:.0f} GB/s = "
         f"{gbs / PEAK_GBS:.1%} of peak")
     del g, body
     torch.cuda.empty_cache()
-    return {"schedule": "norm backwards write partials; one esep_dgamma_reduce_batch after the sweep",
+    return {"schedule": "every norm backward reduces its own weight gradient (2 launches per norm)",
             "ms_per_step": round(ms, 4), "GB/s": round(gbs, 1), "frac_of_peak": round(gbs / PEAK_GBS, 4),
-            "launches_per_step": 4 * CFG4["layers"] + 2 + 2 * CFG4["layers"] + 1}
+            "launches_per_step": 4 * CFG4["layers"] + 2 + 2 * CFG4["layers"] + 1 + 2 * CFG4["layers"] + 1 - 1}
+
+
+def stream_ceiling(dev, cfg, kernel_us, reps):
+    """Per-launch ceiling of one streaming launch at each path kernel's own byte counts and
+    launch pattern: esep_stream_probe (one or two streams read, one written; grid-strided,
+    non-temporal) in a graph of one launch per layer over distinct buffers, the best of three
+    grid sizes, beside the kernel's own per-launch time. Also the step those probes would
+    take with the step's launch counts (a step of pure streaming launches)."""
+    import torch
+
+    from solution.body import _hip
+
+    T, H, HQ, HK, D, L = (cfg[k] for k in ("T", "H", "HQ", "HK", "D", "layers"))
+    e = 2
+    kinds = {  # kernel -> (streams read, bytes per stream, launches per step)
+        "rmsnorm_fwd": (1, e * T * H, 2 * L + 1),
+        "rmsnorm_bwd": (2, e * T * H, 2 * L + 1),
+        "rope_fwd": (1, e * T * (HQ + HK) * D, L),
+        "rope_bwd": (1, e * T * (HQ + HK) * D, L),
+    }
+    out, probe_cache = {}, {}
+    for name, (n_src, nbytes, launches) in kinds.items():
+        key = (n_src, nbytes, launches)
+        if key not in probe_cache:
+            bufs = [[torch.empty(nbytes, device=dev, dtype=torch.uint8) for _ in range(n_src + 1)]
+                    for _ in range(launches)]
+            best = None
+            for blocks in (512, 1024, 2048):
+                def fn(blocks=blocks):
+                    for b in bufs:
+                        _hip.stream_probe(b[0], b[-1], b[1] if n_src == 2 else None, blocks=blocks)
+                gr = capture(fn)
+                time_graph(gr, 2)
+                ms, _ = time_graph(gr, reps)
+                us = ms * 1e3 / launches
+                if best is None or us < best[0]:
+                    best = (us, blocks)
+                del gr
+            del bufs
+            torch.cuda.empty_cache()
+            probe_cache[key] = best
+        us, blocks = probe_cache[key]
+        algo = (n_src + 1) * nbytes
+        k_us = kernel_us.get(name)
+        out[name] = {"probe_us": round(us, 3), "probe_blocks": blocks,
+                     "probe_GB/s": round(algo / (us * 1e-6) / 1e9, 1), "launches_per_step": launches,
+                     "kernel_us": None if k_us is None else round(k_us, 3),
+                     "kernel_over_probe": None if k_us is None else round(k_us / us, 4)}
+        log(f"stream ceiling {name}: probe {us:.2f} us ({blocks} blocks), kernel "
+            f"{k_us if k_us is None else round(k_us, 2)} us")
+    step_ms = sum(v["probe_us"] * v["launches_per_step"] for v in out.values()) * 1e-3
+    return {"what": "esep_stream_probe (out = a (+ b)) at each kernel's bytes and launch pattern, "
+                    "best of 512/1024/2048 blocks of 512 threads",
+            "kernels": out, "probe_step_ms": round(step_ms, 4)}
+
+
+def _flush_buffer(dev):
+    import torch
+
+    return torch.empty(512 << 20, device=dev, dtype=torch.uint8)  # 2x the 256 MB Infinity Cache
+
+
+def time_flushed(g, flush, reps):
+    """Median event time of one replay of graph g with the Infinity Cache flushed before each
+    replay (a 512 MB write outside the timed region)."""
+    import torch
+
+    times = []
+    for _ in range(reps):
+        flush.fill_(1)
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record()
+        g.replay()
+        e1.record()
+        torch.cuda.synchronize()
+        times.append(e0.elapsed_time(e1))
+    return statistics.median(times)
+
+
+def run_small_configs(dev, reps):
+    """Configs 1-3 as whole forward + backward steps, fp16: each timed
+    cache-resident (graph replays back to back; the inputs fit the 256 MB Infinity Cache) and
+    with the cache flushed before each replay (HBM-resident inputs)."""
+    import torch
+
+    from solution.body import _hip
+
+    g = torch.Generator(device=dev).manual_seed(0)
+    hf = torch.float16
+    eps, theta, D = 1e-6, 1e6, 128
+
+    def rn(*shape):
+        return torch.randn(shape, generator=g, device=dev, dtype=torch.float32).to(hf)
+
+    inv = (1.0 / (theta ** (torch.arange(0, D, 2, dtype=torch.float) / D))).to(dev)
+
+    def norm_set(T, H):
+        t = dict(x=rn(T, H), dy=rn(T, H), w=1 + 0.02 * torch.randn(H, generator=g, device=dev))
+        t.update(y=torch.empty(T, H, device=dev, dtype=hf), dx=torch.empty(T, H, device=dev, dtype=hf),
+                 rstd=torch.empty(T, device=dev), dw=torch.empty(H, device=dev),
+                 ws=torch.empty(_hip.rmsnorm_partials(T, H), H, device=dev))
+        return t
+
+    def norm_step(t):
+        _hip.rmsnorm_fwd(t["x"], t["w"], t["y"], eps, rstd=t["rstd"])
+        _hip.rmsnorm_bwd([t["dy"]], t["x"], t["w"], eps, rstd=t["rstd"], dx=t["dx"], dw=t["dw"],
+                         workspace=t["ws"])
+
+    def rope_set(shape_q, shape_k):
+        t = dict(q=rn(*shape_q), k=rn(*shape_k), dqo=rn(*shape_q), dko=rn(*shape_k))
+        for a, b in (("qo", "q"), ("ko", "k"), ("dq", "q"), ("dk", "k")):
+            t[a] = torch.empty_like(t[b])
+        return t
+
+    lens3 = torch.randint(64, 1025, (8,), generator=torch.Generator().manual_seed(0)).tolist()
+    T3 = sum(lens3)
+    cu3 = torch.tensor([0] + list(itertools.accumulate(lens3)), dtype=torch.int32, device=dev)
+    c1 = norm_set(2048, 1536)
+    c2 = rope_set((4, 12, 512, D), (4, 2, 512, D))   # contiguous [B, H, S, D]
+    c3n, c3r = norm_set(T3, 1536), rope_set((1, T3, 12, D), (1, T3, 2, D))
+
+    def rope2(t, sign, src_q, src_k, dst_q, dst_k):
+        # [B, H, S, D] tensors seen as (B, S, H, D) views; positions 0..S-1 per row
+        _hip.rope(t[src_q].transpose(1, 2), t[src_k].transpose(1, 2), t[dst_q].transpose(1, 2),
+                  t[dst_k].transpose(1, 2), inv, sign)
+
+    def c2_step():
+        rope2(c2, 1.0, "q", "k", "qo", "ko")
+        rope2(c2, -1.0, "dqo", "dko", "dq", "dk")
+
+    def c3_step():
+        norm_step(c3n)
+        _hip.rope(c3r["q"], c3r["k"], c3r["qo"], c3r["ko"], inv, 1.0, cu_seqlens=cu3)
+        _hip.rope(c3r["dqo"], c3r["dko"], c3r["dq"], c3r["dk"], inv, -1.0, cu_seqlens=cu3)
+
+    e = 2
+    nb = lambda T, H: norm_fwd_bytes(T, H, e, True) + norm_bwd_bytes(T, H, e, True)  # noqa: E731
+    cases = {
+        "config1": ("RMSNorm fwd + bwd (y, rstd; dx, dw), x [4, 512, 1536] fp16", lambda: norm_step(c1),
+                    nb(2048, 1536), 2048),
+        "config2": ("RoPE fwd + bwd on the padded [B, H, S, D] layout, q [4, 12, 512, 128], k "
+                    "[4, 2, 512, 128] fp16, positions 0..511 per row", c2_step,
+                    2 * rope_bytes(2048, 12, 2, D, e), 2048),
+        "config3": (f"varlen: 8 sequences {lens3} (T={T3}, cu_seqlens int32) RMSNorm [T, 1536] + "
+                    "RoPE q [T, 12, 128] k [T, 2, 128], fp16, fwd + bwd", c3_step,
+                    nb(T3, 1536) + 2 * rope_bytes(T3, 12, 2, D, e), T3),
+    }
+    flush = _flush_buffer(dev)
+    out = {}
+    for name, (what, fn, nbytes, T) in cases.items():
+        gr = capture(fn)
+        time_graph(gr, 3)
+        res_ms, _ = time_graph(gr, reps)
+        fl_ms = time_flushed(gr, flush, reps)
+        row = {"workload": what, "bytes_per_step": nbytes, "tokens": T}
+        for tag, ms in (("cache_resident", res_ms), ("flushed", fl_ms)):
+            gbs = nbytes / (ms * 1e-3) / 1e9
+            row[tag] = {"us_per_step": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
+                        "frac_of_peak": round(gbs / PEAK_GBS, 4), "tokens_per_s": round(T / (ms * 1e-3), 1)}
+        log(f"{name}: cache-resident {res_ms * 1e3:.1f} us, flushed {fl_ms * 1e3:.1f} us per step "
+            f"({nbytes / 1e6:.1f} MB)")
+        out[name] = row
+        del gr
+    del flush, c1, c2, c3n, c3r
+    torch.cuda.empty_cache()
+    return out
 
 
 def run_config4_other_rstd(dev, steps, save_rstd):
@@ -736,16 +913,21 @@ def kernel_rooflines(body, reps):
     on the replay stream. Returns {name: (us_per_launch, algorithmic_bytes_per_launch, launches_per_step)}."""
     c, T = body.cfg, body.T
     L = c["layers"]
+    # With the deferred schedule the norm backward launch is stage 1 (dx and the partials; its
+    # algorithmic bytes exclude the 4H of dw, which stage 2 writes); stage 2 is one batched
+    # launch per step whose algorithmic bytes are the 2L + 1 weight gradients.
+    bwd_bytes = norm_bwd_bytes(T, c["H"], 2, body.save_rstd) - (4 * c["H"] if body.deferred else 0)
     kinds = {
         "rmsnorm_fwd": (lambda: [body.norm_fwd(i) for i in range(2 * L + 1)], 2 * L + 1,
                         norm_fwd_bytes(T, c["H"], 2, body.save_rstd)),
-        "rmsnorm_bwd": (lambda: [body.norm_bwd(i) for i in range(2 * L + 1)], 2 * L + 1,
-                        norm_bwd_bytes(T, c["H"], 2, body.save_rstd)),
+        "rmsnorm_bwd": (lambda: [body.norm_bwd(i) for i in range(2 * L + 1)], 2 * L + 1, bwd_bytes),
         "rope_fwd": (lambda: [body.rope_fwd(l) for l in range(L)], L,
                      rope_bytes(T, c["HQ"], c["HK"], c["D"], 2)),
         "rope_bwd": (lambda: [body.rope_bwd(l) for l in range(L)], L,
                      rope_bytes(T, c["HQ"], c["HK"], c["D"], 2)),
     }
+    if body.deferred:
+        kinds["dgamma_stage2"] = (body.dgamma_stage2, 1, (2 * L + 1) * 4 * c["H"])
     out = {}
     for name, (fn, n, nbytes) in kinds.items():
         g = capture(fn)
@@ -766,6 +948,15 @@ def cpu_baseline(cfg, budget_s=12.0, batch=2):
 
     threads = max(1, min(len(os.sched_getaffinity(0)), 16))
     torch.set_num_threads(threads)
+    model = "unknown"
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
     S, H, HQ, HK, D, eps = (cfg[k] for k in ("S", "H", "HQ", "HK", "D", "eps"))
     B = batch
     T = B * S
@@ -790,7 +981,7 @@ def cpu_baseline(cfg, budget_s=12.0, batch=2):
     layer_bytes = 2 * (norm_fwd_bytes(T, H, e, True) + norm_bwd_bytes(T, H, e, True)) + \
         2 * rope_bytes(T, HQ, HK, D, e)
     return {"value": round(layer_bytes / t / 1e9, 2), "unit": "GB/s", "cores": threads,
-            "kind": "port",
+            "cpu_model": model, "kind": "port",
             "sample": f"one layer of config 4 (2 RMSNorm + q/k RoPE, fwd + autograd bwd) on "
                       f"{B} of its 8 rows (T={T}), fp32 PyTorch eager (HF Qwen2RMSNorm / apply_rotary_pos_emb "
                       f"restated), median of {len(times)} reps, {t * 1e3:.1f} ms per layer; "
@@ -879,12 +1070,25 @@ def main():
                 "us_per_launch": round(us, 3), "bytes_per_launch": nbytes,
                 "all_kernels": {k: {"us": round(v[0], 3), "GB/s": round(v[1] / (v[0] * 1e-6) / 1e9, 1),
                                     "launches_per_step": v[2]} for k, v in kr.items()}}
+    # the same kernel's average duration in the committed rocprofv3 kernel-trace summary of
+    # this workload, when there is one: the fraction from the trace beside the event one
+    ppath = ROOT / "profiles" / "kernel_trace_config4.json"
+    if ppath.exists() and save_rstd:
+        prof = json.loads(ppath.read_text()).get(name)
+        if prof and prof.get("avg_us"):
+            roofline["frac_trace"] = round(nbytes / (prof["avg_us"] * 1e-6) / 1e9 / PEAK_GBS, 4)
+            roofline["trace_avg_us"] = prof["avg_us"]
 
+    c4dims = dict(T=body.T, H=cfg["H"], HQ=cfg["HQ"], HK=cfg["HK"], D=cfg["D"], layers=cfg["layers"])
     del g
     del body
     torch.cuda.empty_cache()
+    ceiling = stream_ceiling(dev, c4dims, {k: v[0] for k, v in kr.items()}, args.kernel_reps)
+    ceiling["step_ms"] = round(ms, 4)
+    ceiling["step_over_probe_step"] = round(ms / ceiling["probe_step_ms"], 4)
+    small = run_small_configs(dev, args.kernel_reps)
     c4_other = run_config4_other_rstd(dev, max(args.steps // 3, 5), not save_rstd)
-    c4_batched = run_config4_batched_dgamma(dev, max(args.steps // 3, 5), save_rstd)
+    c4_per_call = run_config4_per_call_dgamma(dev, max(args.steps // 3, 5), save_rstd)
     c5 = None if args.no_config5 else run_config5(dev, max(args.steps // 3, 5))
     api = run_api_variant(dev, max(args.steps // 3, 5))
     attn = None if args.no_attention else run_attention(dev, max(args.steps // 3, 5))
@@ -912,14 +1116,20 @@ def main():
                    "tokens": T, "batch": cfg["B"], "seq_len": cfg["S"], "hidden": cfg["H"],
                    "q_heads": cfg["HQ"], "kv_heads": cfg["HK"], "head_dim": cfg["D"],
                    "io_dtype": "bf16", "rstd": args.rstd, "graph": True,
+                   "dgamma": "stage 2 deferred to one batched launch per step (the Python API's "
+                             "schedule in a loss.backward() pass, norm_rope.DEFER_WEIGHT_GRAD)",
                    "bytes_per_step": step_bytes},
         "frac_of_peak": round(gbs / PEAK_GBS, 4),
         "tokens_per_s": round(T / (ms * 1e-3), 1),
         "ms_per_step_events": round(ev_ms, 4),
         "roofline": roofline,
         "cpu_baseline": cpu,
+        "stream_ceiling": ceiling,
         "config4_other_rstd": c4_other,
-        "config4_batched_dgamma": c4_batched,
+        "config4_per_call_dgamma": c4_per_call,
+        "config1": small["config1"],
+        "config2": small["config2"],
+        "config3": small["config3"],
         "config5": c5,
         "api_variant": api,
         "attention": attn,

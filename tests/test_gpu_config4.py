@@ -80,15 +80,15 @@ def test_config4_two_layers_through_bench_body(rstd):
         _check_rope(body, l, rows, body.inv_freq)
 
 
-def test_config4_batched_dgamma_equals_fused():
-    """The batched weight-gradient schedule (every norm backward keeps its partials, one
-    esep_dgamma_reduce_batch after the sweep) gives the fused per-norm dw bit for bit, and
-    the same dx."""
+def test_config4_deferred_dgamma_equals_per_call():
+    """The bench's deferred weight-gradient schedule (every norm backward keeps its partials,
+    one esep_dgamma_reduce_batch after the sweep) gives the per-call dw bit for bit, and the
+    same dx."""
     bench = _bench()
     cfg = dict(bench.CFG4, layers=1)
     dev = torch.device(DEV)
-    fused = bench.Body(cfg, True, dev)
-    batched = bench.Body(cfg, True, dev, batched_dgamma=True)
+    fused = bench.Body(cfg, True, dev, deferred_dgamma=False)
+    batched = bench.Body(cfg, True, dev, deferred_dgamma=True)
     fused.step()
     batched.step()
     torch.cuda.synchronize()
