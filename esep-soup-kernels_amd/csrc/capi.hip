@@ -4,6 +4,8 @@
 #include <stdarg.h>
 #include <stdio.h>
 
+#include <mutex>
+
 #include "attention.hpp"
 #include "dropout.hpp"
 #include "esep_body.h"
@@ -305,6 +307,71 @@ int esep_rmsnorm_bwd(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
     if (e != hipSuccess) return hip_fail(e, "rmsnorm_bwd dw reduce launch");
   }
   return 0;
+}
+
+}  // extern "C"
+
+// ---------------------------------------------------------------------------------------
+// Weight-gradient partials of esep_rmsnorm_bwd_noalloc: a file-scope device array (every GPU
+// the library runs on holds its own copy until the process ends). Host code never passes the
+// array's name to a kernel: that is a host-side stand-in, not a device address. Its address on
+// each device is looked up once, with that device current, and kept in g_scratch_ptr.
+// ---------------------------------------------------------------------------------------
+namespace {
+
+constexpr int64_t kScratchFloats = int64_t{2} << 20;  // 8 MiB of fp32 partials per GPU
+constexpr int kScratchDevices = 64;
+static __device__ __align__(256) float scratch[kScratchFloats];
+std::mutex g_scratch_lock;
+float* g_scratch_ptr[kScratchDevices] = {};
+
+// The scratch array's device address on the current device (looked up on first use there).
+int scratch_on_current_device(float** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "rmsnorm_bwd_noalloc: hipGetDevice");
+  if (dev < 0 || dev >= kScratchDevices)
+    return fail(ESEP_EINVAL, "rmsnorm_bwd_noalloc: device %d outside [0, %d)", dev, kScratchDevices);
+  std::lock_guard<std::mutex> guard(g_scratch_lock);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || p == nullptr)
+      return hip_fail(e != hipSuccess ? e : hipErrorInvalidSymbol,
+                      "rmsnorm_bwd_noalloc: hipGetSymbolAddress(scratch)");
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int esep_rmsnorm_bwd_noalloc(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
+                             const float* dr_out, const void* x, int x_dt, int64_t ld_x,
+                             int from_y, const float* rstd, const float* w, const int32_t* slot,
+                             const float* xs, int n_special, float* dr_f32, void* dx_lp,
+                             int dx_dt, int64_t ld_out, void* dw, int dw_dt, int64_t rows,
+                             int64_t n, float eps, void* stream) {
+  g_err[0] = 0;
+  if (dw == nullptr)
+    return fail(ESEP_EINVAL, "rmsnorm_bwd_noalloc: dw is required (without a weight gradient "
+                "esep_rmsnorm_bwd needs no workspace)");
+  if (n < 1 || n > ESEP_NORM_MAX_COLS || rows < 0)
+    return fail(ESEP_ESHAPE, "rmsnorm_bwd_noalloc: rows=%lld, n=%lld", (long long)rows, (long long)n);
+  const int64_t P = bwd_partials(rows, n);
+  if (P * n > kScratchFloats)
+    return fail(ESEP_ESHAPE, "rmsnorm_bwd_noalloc: %lld x %lld partials exceed the %lld-float "
+                "scratch (use esep_rmsnorm_bwd with a workspace)", (long long)P, (long long)n,
+                (long long)kScratchFloats);
+  float* part = nullptr;
+  const int rc = scratch_on_current_device(&part);
+  if (rc != 0) return rc;
+  return esep_rmsnorm_bwd(dys, n_dy, dy_dt, ld_dy, dr_out, x, x_dt, ld_x, from_y, rstd, w, slot,
+                          xs, n_special, dr_f32, dx_lp, dx_dt, ld_out, part, rows > 0 ? P : 0,
+                          dw, dw_dt, rows, n, eps, stream);
 }
 
 int esep_dgamma_reduce(const float* partials, int64_t n_partials, int64_t n, void* dw, int dw_dt,

@@ -41,6 +41,9 @@ SIGNATURES = {
     "esep_rmsnorm_bwd": (_i32, [_vp, _i32, _i32, _i64, _vp, _vp, _i32, _i64, _i32, _vp, _vp, _vp,
                                 _vp, _i32, _vp, _vp, _i32, _i64, _vp, _i64, _vp, _i32, _i64, _i64,
                                 _f32, _vp]),
+    "esep_rmsnorm_bwd_noalloc": (_i32, [_vp, _i32, _i32, _i64, _vp, _vp, _i32, _i64, _i32, _vp,
+                                        _vp, _vp, _vp, _i32, _vp, _vp, _i32, _i64, _vp, _i32,
+                                        _i64, _i64, _f32, _vp]),
     "esep_dgamma_reduce": (_i32, [_vp, _i64, _i64, _vp, _i32, _vp]),
     "esep_dgamma_reduce_batch": (_i32, [_vp, _i32, _i64, _i32, _vp]),
     "esep_attn_fwd": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i32, _i64, _i32,

@@ -128,6 +128,30 @@ int esep_rmsnorm_bwd(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
                      int64_t rows, int64_t n, float eps, void* stream);
 
 /*
+ * esep_rmsnorm_bwd with a weight gradient, allocating nothing: the [P, n] fp32 partials live in a
+ * scratch array inside the library (8 MiB of device memory on every GPU the library runs on,
+ * held until the process ends), so the caller passes no workspace. No counterpart in the
+ * reference; it is for callers that cannot allocate device memory (code under HIP graph
+ * capture that may not call hipMalloc, tight serving loops, harnesses that forbid allocation).
+ * Arguments are those of esep_rmsnorm_bwd without dw_partials / n_partials; dw is required.
+ * Limit: esep_rmsnorm_partials(rows, n) * n <= 2^21 floats (config 4's 8192 x 1536 and config
+ * 5's 65536 x 3584 fit), else ESEP_ESHAPE. The scratch array belongs to the device current on
+ * the calling thread (the stream must be on that device); its address is looked up there on
+ * the first call. Every call fully writes the partials it then reads, but all calls on one GPU
+ * share the array: calls that can overlap on one GPU (on different streams, or from threads
+ * that do not order their streams) race and must not be issued.
+ */
+int esep_rmsnorm_bwd_noalloc(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
+                             const float* dr_out,
+                             const void* x, int x_dt, int64_t ld_x, int from_y,
+                             const float* rstd,
+                             const float* w,
+                             const int32_t* slot, const float* xs, int n_special,
+                             float* dr_f32, void* dx_lp, int dx_dt, int64_t ld_out,
+                             void* dw, int dw_dt,
+                             int64_t rows, int64_t n, float eps, void* stream);
+
+/*
  * Stage 2 of the weight gradient on its own: dw[j] = sum_{p < n_partials} partials[p, j], summed
  * in an order that depends on n_partials only (bitwise equal to the stage 2 inside
  * esep_rmsnorm_bwd for the same partials). partials: fp32 [n_partials, n] contiguous and
