@@ -1,35 +1,37 @@
-"""Pad removal inside one batch for the Qwen2 decoder, with the norms and RoPE on this
-repository's HIP kernels: the reference's patch point (gojosatorukz/esep-soup-kernels,
-solution/body/packed.py), rebuilt around norm_rope.py.
+"""The reference's patch point (solution/body/packed.py): Qwen2Model.forward replaced by a
+pad-free decoder whose norms, RoPE, attention and SwiGLU run on this repository's HIP kernels.
 
-`Qwen2Model.forward` is class-patched (`patch()`, reference packed.py:843-875). For a normal
-training batch (2-D attention mask, no cache, no captured outputs) the real tokens of all rows
-are packed into one [1, T, H] sequence, every token-wise op of the decoder layers runs on the
-T real tokens only, attention runs per row on that row's slice with a causal mask, and the
-final hidden states are scattered back to [B, L, H] with zeros at the pad positions
-(reference packed.py:800-840). Anything unusual goes to the original forward.
+`patch()` swaps Qwen2Model.forward (a class patch; the original stays reachable as
+forward.__wrapped__). For a training-style call (2-D CUDA input_ids and attention mask, no
+cache, no captured hidden states or attentions) the real tokens of all rows are gathered into
+one packed [1, T, H] stream, every token-wise piece of the decoder layers runs on those T
+tokens, attention runs causally within each original row, and the final hidden states are
+scattered back to [B, L, H] with zeros at the pads. Any other call runs the original forward.
 
-Pieces and their guards (each falls back to the HF / torch op when its inputs are not what the
-kernel takes, as the reference's do):
-  _add_norm   residual add + RMSNorm on norm_rope.add_rmsnorm (fp32 residual stream, a plain
-              Qwen2RMSNorm without hooks, row width <= NORM_BLOCK). Unlike the reference, a
-              trainable norm weight stays on the kernel: it gets its gradient from the kernel's
-              deterministic two-stage reduction (the reference sends it to HF, packed.py:129).
-  _rope       norm_rope.rope on the packed positions and the model's inv_freq (HF default rope
-              type with attention_scaling 1.0), fp16 / bf16 / fp32 q and k.
-  _attention  attention.varlen_attention: causal attention over all rows in one launch per
-              direction (fp16 / bf16, head_dim 64 or 128, no dropout); else the reference's
-              per-row SDPA loop.
-  _mlp        frozen projections: _RecomputeMLP (saves no [T, intermediate] tensor, recomputes
-              the gate / up projections and, when the norm did not save its output, the norm
-              itself in backward); otherwise the model's projections with silu(g) * u on the
-              HIP SwiGLU kernel (solution/swiglu.py).
-The q/k/v/o projections call the model's own modules: the reference's NF4 / LoRA routes
-(packed.py:184-352, :440-524) are other workstreams and are not part of this build; their flags
-exist for API compatibility.
+Per decoder layer, each piece has a guard and an HF / torch fallback (warned once per
+(piece, reason) while training; reference packed.py:62-96):
+  norms       norm_rope.add_rmsnorm: residual add fused into the RMSNorm on an fp32 residual
+              stream; the decoder-layer norms return one copy of their output per consumer (5 after
+              the input norm: q / k / v projections and the q / v LoRA inputs; 2 after the
+              post-attention norm: gate and up) so their gradients are summed in the norm
+              backward. A trainable norm weight stays on the kernel (its gradient comes from the
+              kernel's two-stage reduction); the reference hands it to HF (its packed.py:129).
+  q/k/v       the model's projections; a peft-style LoRA projection (base_layer + lora_A /
+              lora_B / lora_dropout / scaling, one active adapter) runs its base layer directly
+              and its LoRA term on lora.py: v's added into the base output, q's passed to the
+              RoPE kernel as q_delta (reference packed.py:240-352).
+  RoPE        norm_rope.rope on the packed positions with the model's inv_freq.
+  attention   attention.varlen_attention over all rows in one launch per direction; else a
+              per-row SDPA loop (reference packed.py:404-436).
+  MLP         frozen plain projections: _RecomputeMLP (no [T, intermediate] tensor saved);
+              otherwise the projections with the HIP SwiGLU, gate and up fed from their own
+              copies of the norm output.
+The NF4 / bitsandbytes projection routes of the reference (its packed.py:184-238, :440-561)
+need bitsandbytes, which this build does not have; those projections run as modules.
 """
 
 import contextlib
+import functools
 import logging
 
 import torch
@@ -37,17 +39,11 @@ import torch.nn.functional as F
 
 log = logging.getLogger(__name__)
 
-# Keyword arguments that may reach Qwen2Model.forward in a training step and that the packed
-# path can ignore (reference packed.py:59-60). Anything else -> original forward.
-_IGNORED_KWARGS = {"num_items_in_batch", "return_dict", "output_attentions",
-                   "output_hidden_states", "is_causal"}
-
-# In-process switches (never read from the environment), as in the reference: USE_KERNELS
-# (packed.py:106) turns the HIP norm / RoPE off (packed layout on torch ops);
-# NORM_SAVE_OUTPUT (:149) makes the decoder-layer norms save their 16-bit output instead of the
-# fp32 residual; RECOMPUTE_MLP (:448) sends an MLP with frozen projections through
-# _RecomputeMLP; USE_LORA_KERNELS (:186) selects a route this build does not have (kept so code
-# that sets it keeps working).
+# Switches read at call time (never from the environment), as the reference's: USE_KERNELS
+# (packed.py:106) turns every HIP piece off (the packed layout on torch ops);
+# NORM_SAVE_OUTPUT (:149) makes the decoder-layer norms save their 16-bit output instead of
+# the fp32 residual; USE_LORA_KERNELS (:186) runs LoRA projections as modules when off;
+# RECOMPUTE_MLP (:448) sends frozen MLPs through _RecomputeMLP.
 USE_KERNELS = True
 NORM_SAVE_OUTPUT = True
 USE_LORA_KERNELS = True
@@ -55,33 +51,46 @@ RECOMPUTE_MLP = True
 
 _KERNEL_FLOATS = (torch.float16, torch.bfloat16, torch.float32)
 
+# Keyword arguments of Qwen2Model.forward that a training step may pass and that the packed
+# path can ignore (reference packed.py:59-60); any other one selects the original forward.
+_IGNORED_KWARGS = {"num_items_in_batch", "return_dict", "output_attentions",
+                   "output_hidden_states", "is_causal"}
+
+# Messages already logged by this process (keys: "active", a full-fallback reason, or
+# "piece: reason"); a module-level set so that tests can reset it.
 _warned = set()
-# [training, layer index or "final norm"], set by packed_forward for the warn-once messages.
-_WHERE = [False, None]
+
+
+class _Report:
+    """Where the packed forward is (training or not, which layer) for the warn-once log."""
+
+    training = False
+    where = None
+
+    @classmethod
+    def once(cls, key, message, *args):
+        if key not in _warned:
+            _warned.add(key)
+            log.warning(message, *args)
 
 
 def _warn_once(reason):
-    if reason not in _warned:
-        _warned.add(reason)
-        log.warning("solution.body.packed: original Qwen2Model.forward used (%s)", reason)
+    """The whole call went to the original forward."""
+    _Report.once(reason, "solution.body.packed: original Qwen2Model.forward used (%s)", reason)
 
 
 def _fallback(piece, reason):
-    """A guard sent `piece` to the HF / torch op: one warning per (piece, reason) in training,
-    naming the first layer seen (reference packed.py:76-87). Returns None."""
-    if _WHERE[0]:
-        key = f"{piece}: {reason}"
-        if key not in _warned:
-            _warned.add(key)
-            log.warning("solution.body.packed: %s not used (%s; first at layer %s)", piece,
-                        reason, _WHERE[1])
+    """A guard sent one piece of the packed forward to its HF / torch op. Logged once per
+    (piece, reason) and only while training, naming the first layer it happened at. Returns
+    None so that guards can `return _fallback(...)`."""
+    if _Report.training:
+        _Report.once(f"{piece}: {reason}", "solution.body.packed: %s not used (%s; first at layer %s)",
+                     piece, reason, _Report.where)
     return None
 
 
 def _note_active():
-    if "active" not in _warned:
-        _warned.add("active")
-        log.warning("solution.body: packed decoder active (pad removal + own kernels)")
+    _Report.once("active", "solution.body: packed decoder active (pad removal + own kernels)")
 
 
 def _has_hooks(module):
@@ -89,6 +98,9 @@ def _has_hooks(module):
                 or getattr(module, "_forward_hooks_with_kwargs", None))
 
 
+# ----------------------------------------------------------------------------------------
+# norms
+# ----------------------------------------------------------------------------------------
 def _is_rmsnorm(norm):
     from transformers.models.qwen2.modeling_qwen2 import Qwen2RMSNorm
 
@@ -98,26 +110,26 @@ def _is_rmsnorm(norm):
 
 
 def _norm_eps(norm, residual, delta):
-    """`variance_epsilon` if add_rmsnorm can replace `norm(residual + delta)`, else None
-    (reference packed.py:111-140): a plain Qwen2RMSNorm without hooks, a 1-D float weight on the
-    residual's device, an fp32 device residual (a 16-bit residual stream keeps HF's rounding by
-    falling back), row width <= NORM_BLOCK, and a float delta of the residual's shape."""
+    """The norm's eps when add_rmsnorm can stand in for norm(residual + delta), else None
+    (reference packed.py:111-140): an unmodified RMSNorm module without hooks with a 1-D
+    floating weight on the device, an fp32 residual stream on the device (a 16-bit stream keeps
+    HF's rounding), rows within NORM_BLOCK, and a floating delta shaped like the residual."""
     if not USE_KERNELS:
         return None
     from .norm_rope import NORM_BLOCK
 
     if not _is_rmsnorm(norm) or _has_hooks(norm):
         return _fallback("norm kernel", "not a plain Qwen2RMSNorm or hooks")
-    w = getattr(norm, "weight", None)
-    eps = getattr(norm, "variance_epsilon", None)
-    if not isinstance(w, torch.Tensor) or eps is None:
+    weight, eps = getattr(norm, "weight", None), getattr(norm, "variance_epsilon", None)
+    if not isinstance(weight, torch.Tensor) or eps is None:
         return _fallback("norm kernel", "missing weight / eps")
-    if w.dim() != 1 or w.dtype not in _KERNEL_FLOATS or not w.is_cuda:
-        return _fallback("norm kernel", f"weight {w.dtype} {tuple(w.shape)}")
-    if residual.dtype != torch.float32 or not residual.is_cuda or residual.shape[-1] != w.shape[0]:
+    if weight.dim() != 1 or weight.dtype not in _KERNEL_FLOATS or not weight.is_cuda:
+        return _fallback("norm kernel", f"weight {weight.dtype} {tuple(weight.shape)}")
+    hidden = weight.shape[0]
+    if residual.dtype != torch.float32 or not residual.is_cuda or residual.shape[-1] != hidden:
         return _fallback("norm kernel", f"residual {residual.dtype} {residual.device}")
-    if w.shape[0] > NORM_BLOCK:
-        return _fallback("norm kernel", f"hidden {w.shape[0]} > {NORM_BLOCK}")
+    if hidden > NORM_BLOCK:
+        return _fallback("norm kernel", f"hidden {hidden} > {NORM_BLOCK}")
     if delta is not None and (delta.dtype not in _KERNEL_FLOATS or delta.shape != residual.shape
                               or delta.device != residual.device):
         return _fallback("norm kernel", f"delta {delta.dtype} {tuple(delta.shape)}")
@@ -125,12 +137,12 @@ def _norm_eps(norm, residual, delta):
 
 
 def _add_norm(norm, residual, delta, final=False, with_eps=False, n_out=1, save_output=False):
-    """`r = residual + delta` (delta may be None); returns (r, norm(r)) (+ eps with with_eps:
-    the eps the kernel used, or None when HF's norm ran). Kernel path: r stays fp32; the normed
-    output of a decoder-layer norm is stored in the autocast dtype (it only feeds projections,
-    which compute in it); the final norm's output has HF's dtype promote(weight, residual).
-    n_out > 1: n_out outputs, one per consumer (kernel: views whose gradients the norm backward
-    sums; HF: the same tensor n_out times). Reference packed.py:152-181."""
+    """(r, norm(r)) for r = residual (+ delta); with with_eps also the eps the kernel used (None
+    when HF's norm ran). With n_out > 1 the normed output comes as a tuple of n_out tensors, one
+    per consumer (the kernel's are views whose gradients its backward sums; HF's are the same
+    tensor repeated). The kernel keeps r in fp32; the normed output of a decoder-layer norm is
+    stored in the autocast dtype (its consumers compute in it), the final norm's in HF's
+    promote(weight, residual). Reference packed.py:152-181."""
     eps = _norm_eps(norm, residual, delta)
     if eps is not None:
         out_dtype = torch.promote_types(norm.weight.dtype, residual.dtype)
@@ -142,152 +154,222 @@ def _add_norm(norm, residual, delta, final=False, with_eps=False, n_out=1, save_
             r, y = add_rmsnorm(residual, delta, norm.weight, eps, out_dtype, n_out,
                                save_output=save_output and not final)
             return (r, y, eps) if with_eps else (r, y)
-    if delta is not None:
-        residual = residual + delta
-    y = norm(residual)
-    if n_out > 1:
-        y = (y,) * n_out
-    return (residual, y, None) if with_eps else (residual, y)
+    r = residual if delta is None else residual + delta
+    y = norm(r)
+    ys = y if n_out == 1 else (y,) * n_out
+    return (r, ys, None) if with_eps else (r, ys)
 
 
+# ----------------------------------------------------------------------------------------
+# projections and their LoRA terms
+# ----------------------------------------------------------------------------------------
+def _lora_route(module, x):
+    """How a projection runs on the packed 16-bit x [1, T, in]:
+      (base layer, None)              a LoRA wrapper with no adapter active: its base alone;
+      (base layer, (A, B, p, scale))  a LoRA wrapper this path runs (lora.lora_params);
+      None                            anything else, or a guard failed: module(x).
+    A LoRA wrapper is any module with peft's LoRA layer attributes (base_layer, lora_A, lora_B,
+    lora_dropout, scaling, active_adapters) whose base is a plain nn.Linear. The path needs the
+    kernels on, a device x in fp16 / bf16 under autocast to that dtype (peft computes the term
+    in the autocast dtype then), and no hooks (reference packed.py:240-290)."""
+    if not (USE_KERNELS and USE_LORA_KERNELS):
+        return None
+    base = getattr(module, "base_layer", None)
+    if base is None or not hasattr(module, "lora_A"):
+        return None
+    if x.dtype not in (torch.float16, torch.bfloat16) or not x.is_cuda:
+        return _fallback("LoRA path", f"x {x.dtype} {x.device}")
+    if not torch.is_autocast_enabled("cuda") or torch.get_autocast_dtype("cuda") != x.dtype:
+        return _fallback("LoRA path", f"no autocast to {x.dtype}")
+    if _has_hooks(module) or type(base) is not torch.nn.Linear or _has_hooks(base):
+        return _fallback("LoRA path", f"{type(module).__name__} / {type(base).__name__} or hooks")
+    if getattr(module, "disable_adapters", False) or getattr(module, "merged", False):
+        return _fallback("LoRA path", "adapters disabled or merged")
+    if not any(name in module.lora_A for name in getattr(module, "active_adapters", ())):
+        return base, None
+    from .lora import lora_params
+
+    params = lora_params(module)
+    if params is None:
+        return _fallback("LoRA path", "adapter config (lora.lora_params)")
+    return base, params
+
+
+def _project(module, x, x_lora=None):
+    """module(x) for x [1, T, in] -> [1, T, out]. A routed LoRA projection runs its base on the
+    2-D x (a fresh output: F.linear with a bias on a 3-D input can return a view) and adds its
+    LoRA term into that output; x_lora is the LoRA term's own copy of the norm output (same
+    values), so the two input gradients reach the norm backward apart."""
+    route = _lora_route(module, x)
+    if route is None:
+        return module(x)
+    base, params = route
+    x2 = x.reshape(-1, x.shape[-1])
+    out = base(x2)
+    if params is not None:
+        from .lora import LoRAFunction
+
+        xl = x2 if x_lora is None else x_lora.reshape(-1, x_lora.shape[-1])
+        out = LoRAFunction.apply(xl, out, *params)
+    return out.view(1, x2.shape[0], -1)
+
+
+def _project_q(module, x, x_lora=None):
+    """(q [1, T, out], LoRA term [1, T, out] or None) for q_proj. The term is not added here:
+    the RoPE kernel adds it to q before rotating, and its backward hands the same pre-rotation
+    gradient to both. Without a routed LoRA, q is module(x) (its LoRA included)."""
+    route = _lora_route(module, x)
+    if route is None or route[1] is None:
+        return _project(module, x), None
+    base, params = route
+    from .lora import LoRADeltaFunction
+
+    x2 = x.reshape(-1, x.shape[-1])
+    q = base(x2)
+    xl = x2 if x_lora is None else x_lora.reshape(-1, x_lora.shape[-1])
+    term = LoRADeltaFunction.apply(xl, *params)
+    return q.view(1, x2.shape[0], -1), term.view(1, x2.shape[0], -1)
+
+
+# ----------------------------------------------------------------------------------------
+# rotary embedding
+# ----------------------------------------------------------------------------------------
 class _RopeInputs:
-    """What RoPE needs for one packed forward (reference packed.py:355-379): the kernel's
-    (positions [T] int64, inv_freq fp32) when the rotary embedding is HF's default type with
-    attention_scaling 1.0 (Qwen2.5), else HF's cos/sin, built lazily once."""
+    """The rotary inputs of one packed forward (reference packed.py:355-379): the kernel's
+    (positions [T] int64, fp32 inv_freq) when the model's rotary embedding is HF's default type
+    with attention_scaling 1 and a head dim the kernel takes, else HF's cos / sin, built once
+    on first use."""
 
     def __init__(self, model, hidden, pos):
-        self.rotary, self.hidden, self.pos = model.rotary_emb, hidden, pos  # pos [1, T] int64
-        self.positions = self.inv_freq = None
+        rotary = model.rotary_emb
+        self._rotary, self._hidden, self._pos = rotary, hidden, pos
         self._cos_sin = None
-        rot = self.rotary
-        inv = getattr(rot, "inv_freq", None)
-        hd = getattr(model.config, "head_dim", None) or \
-            model.config.hidden_size // model.config.num_attention_heads
-        if (USE_KERNELS and type(rot).__name__ == "Qwen2RotaryEmbedding" and not _has_hooks(rot)
-                and getattr(rot, "rope_type", None) == "default"
-                and getattr(rot, "attention_scaling", None) == 1.0
-                and isinstance(inv, torch.Tensor) and inv.is_cuda and inv.dim() == 1
-                and hd in (64, 128, 256) and inv.shape[0] == hd // 2):
+        self.positions = self.inv_freq = None
+        cfg = model.config
+        head_dim = getattr(cfg, "head_dim", None) or cfg.hidden_size // cfg.num_attention_heads
+        inv = getattr(rotary, "inv_freq", None)
+        kernel_ok = (USE_KERNELS and type(rotary).__name__ == "Qwen2RotaryEmbedding"
+                     and not _has_hooks(rotary) and getattr(rotary, "rope_type", None) == "default"
+                     and getattr(rotary, "attention_scaling", None) == 1.0
+                     and isinstance(inv, torch.Tensor) and inv.is_cuda and inv.dim() == 1
+                     and head_dim in (64, 128, 256) and inv.shape[0] == head_dim // 2)
+        if kernel_ok:
             self.positions = pos.reshape(-1)
             self.inv_freq = inv.detach().to(torch.float32).contiguous()
 
     def cos_sin(self):
         if self._cos_sin is None:
-            self._cos_sin = self.rotary(self.hidden, self.pos)
+            self._cos_sin = self._rotary(self._hidden, self._pos)
         return self._cos_sin
 
 
 def _rope(q, k, rope_in, q_delta=None):
-    """RoPE on q [1, T, Hq, D] and k [1, T, Hk, D] -> same shapes (reference packed.py:382-401).
-    squeeze(0), not [0]: a view whose backward is a view too."""
-    if (rope_in.positions is not None and q.dtype in _KERNEL_FLOATS and k.dtype == q.dtype
-            and q.is_cuda and (q_delta is None or q_delta.dtype == q.dtype)):
+    """Rotated (q + q_delta, k) for q [1, T, Hq, D], k [1, T, Hk, D] (reference
+    packed.py:382-401): on the kernel when it takes these inputs (the add happens inside it,
+    in q's dtype), else HF's apply_rotary_pos_emb after the add."""
+    kernel_ok = (rope_in.positions is not None and q.dtype in _KERNEL_FLOATS and q.is_cuda
+                 and k.dtype == q.dtype and (q_delta is None or q_delta.dtype == q.dtype))
+    if kernel_ok:
         from .norm_rope import rope
 
+        # squeeze, not indexing: its backward is a view too
         qo, ko = rope(q.squeeze(0), k.squeeze(0), rope_in.positions, rope_in.inv_freq,
                       q_delta=None if q_delta is None else q_delta.squeeze(0))
         return qo.unsqueeze(0), ko.unsqueeze(0)
-    if q_delta is not None:
-        q = q + q_delta.view_as(q)
     from transformers.models.qwen2.modeling_qwen2 import apply_rotary_pos_emb
 
+    if q_delta is not None:
+        q = q + q_delta.view_as(q)
     cos, sin = rope_in.cos_sin()
     return apply_rotary_pos_emb(q, k, cos, sin, unsqueeze_dim=2)
 
 
-_CU_CACHE = {}  # (device, lens) -> cu_seqlens of the current batch (one entry)
-
-
+# ----------------------------------------------------------------------------------------
+# attention
+# ----------------------------------------------------------------------------------------
+@functools.lru_cache(maxsize=4)
 def _cu_seqlens(lens, device):
-    key = (device, tuple(lens))
-    cu = _CU_CACHE.get(key)
-    if cu is None:
-        from .attention import cu_seqlens_from_lengths
+    """int32 [n + 1] sequence offsets of the packed rows (cached for the few recent batches)."""
+    from .attention import cu_seqlens_from_lengths
 
-        _CU_CACHE.clear()
-        cu = _CU_CACHE[key] = cu_seqlens_from_lengths(lens, device)
-    return cu
+    return cu_seqlens_from_lengths(list(lens), device)
 
 
 def _attention(attn, q, k, v, lens):
-    """Causal attention per original row on its packed slice. q [1, T, Hq, D], k/v [1, T, Hk, D]
-    -> [1, T, Hq * D]. GQA: query head h uses kv head h // (Hq / Hk), as HF's repeat_kv.
-    With the kernels on (fp16 / bf16, D in {64, 128}, no dropout) every row runs in one varlen
-    launch (attention.varlen_attention); otherwise per row through torch's SDPA with the kv
-    heads broadcast by a zero stride (reference packed.py:404-436)."""
+    """Causal attention within each original row of the packed q [1, T, Hq, D] and k, v
+    [1, T, Hk, D] -> [1, T, Hq * D]; query head h reads kv head h // (Hq / Hk) (HF's repeat_kv).
+    One varlen kernel launch per direction when it applies, else torch's SDPA per row
+    (reference packed.py:404-436)."""
     if torch.is_autocast_enabled("cuda"):
         dt = torch.get_autocast_dtype("cuda")
         q, k, v = q.to(dt), k.to(dt), v.to(dt)
-    hq, hk, d = q.shape[2], k.shape[2], q.shape[3]
-    groups = hq // hk
+    n_tok, hq, d = q.shape[1], q.shape[2], q.shape[3]
     dropout = attn.attention_dropout if attn.training else 0.0
     if USE_KERNELS:
         from . import attention
 
         if attention.supported(q, k, v, dropout):
-            o = attention.varlen_attention(q, k, v, _cu_seqlens(lens, q.device), max(lens),
+            o = attention.varlen_attention(q, k, v, _cu_seqlens(tuple(lens), q.device), max(lens),
                                            attn.scaling)
-            return o.view(1, o.shape[0], hq * d)
+            return o.view(1, n_tok, hq * d)
         _fallback("attention kernel", f"dtype {q.dtype}, head_dim {d}, dropout {dropout}")
-    outs = []
-    for qr, kr, vr in zip(q.squeeze(0).split(lens), k.squeeze(0).split(lens),
-                          v.squeeze(0).split(lens)):
-        n = qr.shape[0]
-        qh = qr.reshape(n, hk, groups, d).permute(1, 2, 0, 3)               # [Hk, G, n, D]
-        kh = kr.permute(1, 0, 2).unsqueeze(1).expand(hk, groups, n, d)
-        vh = vr.permute(1, 0, 2).unsqueeze(1).expand(hk, groups, n, d)
-        o = F.scaled_dot_product_attention(qh, kh, vh, dropout_p=dropout, is_causal=True,
-                                           scale=attn.scaling)
-        outs.append(o.permute(2, 0, 1, 3))                                  # [n, Hk, G, D]
-    out = torch.cat(outs, dim=0) if len(outs) > 1 else outs[0].contiguous()
-    return out.reshape(1, out.shape[0], hq * d)
+    rows = []
+    for qs, ks, vs in zip(q[0].split(lens), k[0].split(lens), v[0].split(lens)):
+        # [n, H, D] row slices as [1, H, n, D]; SDPA's grouped-query mode maps query head h to
+        # kv head h // (Hq / Hk)
+        o = F.scaled_dot_product_attention(qs.transpose(0, 1)[None], ks.transpose(0, 1)[None],
+                                           vs.transpose(0, 1)[None], dropout_p=dropout,
+                                           is_causal=True, scale=attn.scaling, enable_gqa=True)
+        rows.append(o[0].transpose(0, 1))  # [n, Hq, D]
+    return torch.cat(rows).reshape(1, n_tok, hq * d)
 
 
+# ----------------------------------------------------------------------------------------
+# MLP
+# ----------------------------------------------------------------------------------------
 def _plain_silu_mlp(mlp, x):
-    """An unmodified Qwen2MLP with silu and no hooks, on a CUDA input."""
+    """An unmodified silu Qwen2MLP without hooks, on a device input."""
     from transformers.models.qwen2.modeling_qwen2 import Qwen2MLP
 
-    return (type(mlp) is Qwen2MLP and not _has_hooks(mlp) and x.is_cuda
-            and getattr(getattr(mlp, "config", None), "hidden_act", None) == "silu")
+    act = getattr(getattr(mlp, "config", None), "hidden_act", None)
+    return type(mlp) is Qwen2MLP and not _has_hooks(mlp) and x.is_cuda and act == "silu"
 
 
 def _mlp_layers(mlp, x):
-    """(gate, up, down) when the recompute MLP applies to mlp(x), else None (reference
-    packed.py:493-524, there for frozen NF4 projections): kernels and RECOMPUTE_MLP on, grad
-    mode on, an unmodified silu Qwen2MLP whose projections are exactly nn.Linear without bias
-    or hooks, no trainable parameter in the block, and an fp16 / bf16 CUDA x that the
-    projections compute in (autocast to x's dtype, or weights of x's dtype)."""
+    """(gate, up, down) when mlp(x) can run as _RecomputeMLP, else None (reference
+    packed.py:493-524, where the projections are frozen NF4): the kernels and RECOMPUTE_MLP on,
+    grad mode on, a plain silu Qwen2MLP whose three projections are bias-free nn.Linear without
+    hooks, nothing in it trainable, and a 16-bit device x that the projections compute in
+    (autocast to x's dtype, or weights of x's dtype)."""
     if not (USE_KERNELS and RECOMPUTE_MLP) or not torch.is_grad_enabled():
         return None
-    why = "recompute MLP"
+    piece = "recompute MLP"
     if x.dtype not in (torch.float16, torch.bfloat16) or not _plain_silu_mlp(mlp, x):
-        return _fallback(why, f"x {x.dtype}, {type(mlp).__name__}, hooks or activation")
-    layers = (getattr(mlp, "gate_proj", None), getattr(mlp, "up_proj", None),
-              getattr(mlp, "down_proj", None))
-    autocast = torch.is_autocast_enabled("cuda") and torch.get_autocast_dtype("cuda") == x.dtype
-    for lin in layers:
+        return _fallback(piece, f"x {x.dtype}, {type(mlp).__name__}, hooks or activation")
+    projections = (mlp.gate_proj, mlp.up_proj, mlp.down_proj)
+    autocast_to_x = (torch.is_autocast_enabled("cuda")
+                     and torch.get_autocast_dtype("cuda") == x.dtype)
+    for lin in projections:
         if type(lin) is not torch.nn.Linear or _has_hooks(lin) or lin.bias is not None:
-            return _fallback(why, "projection not a plain bias-free nn.Linear")
-        if not autocast and lin.weight.dtype != x.dtype:
-            return _fallback(why, f"weights {lin.weight.dtype} without autocast to {x.dtype}")
-    if any(q.requires_grad for q in mlp.parameters()):
-        return _fallback(why, "trainable parameter in the MLP")
-    return layers
+            return _fallback(piece, "projection not a plain bias-free nn.Linear")
+        if not autocast_to_x and lin.weight.dtype != x.dtype:
+            return _fallback(piece, f"weights {lin.weight.dtype} without autocast to {x.dtype}")
+    if any(prm.requires_grad for prm in mlp.parameters()):
+        return _fallback(piece, "trainable parameter in the MLP")
+    return projections
 
 
 class _RecomputeMLP(torch.autograd.Function):
-    """down(silu(gate(x)) * up(x)) for frozen projections, saving nothing of size
-    [T, intermediate] (reference packed.py:562-643; there the projections are frozen NF4, here
-    frozen fp16 / bf16 nn.Linear, as in a LoRA run on an unquantized base).
+    """down(silu(gate(x)) * up(x)) for frozen projections without saving any [T, intermediate]
+    tensor (the reference's activation-memory trade, packed.py:562-643, for its frozen NF4
+    projections; here frozen 16-bit nn.Linear, a LoRA run on an unquantized base).
 
-    forward: g = x Wg^T, u = x Wu^T, h = silu(g) * u (HIP kernel, in place into g), out = h Wd^T.
-    Saved: x itself (when the norm saves its output, the same tensor: no extra memory), or the
-    norm's fp32 input r and weight, x then recomputed in backward by the same norm kernel
-    (bit-exact, norm_rope.rmsnorm_recompute).
-    backward: dh = dout Wd; g, u recomputed; (dg, du) = swiglu backward (HIP kernel, in place
-    into g, u); dx_gate = dg Wg, dx_up = du Wu, returned as the grads of the two fan-out copies
-    x_gate, x_up (the norm backward sums them; one tensor for both: autograd sums them).
-    """
+    apply(x_gate, x_up, r, w_norm, eps, gate, up, down). Saved: x itself, or (when the norm
+    that produced x did not keep its output) the norm's fp32 input r and weight, x then being
+    recomputed bit-exactly by the same norm kernel in backward. Forward: g, u from the two
+    projections, h = silu(g) * u on the HIP kernel (into g), out = h down^T. Backward: dh =
+    dout down, g and u recomputed, (dg, du) by the HIP kernel in place, dx_gate = dg gate and
+    dx_up = du up, returned for the two fan-out copies (the norm backward sums them)."""
 
     @staticmethod
     @torch.amp.custom_fwd(device_type="cuda")
@@ -296,18 +378,17 @@ class _RecomputeMLP(torch.autograd.Function):
 
         shape = x.shape
         x2 = x.reshape(-1, shape[-1])
-        g = F.linear(x2, gate.weight).contiguous()
+        h = F.linear(x2, gate.weight).contiguous()
         u = F.linear(x2, up.weight).contiguous()
-        _hip.swiglu_fwd(g, u, g)
-        del u
-        out = F.linear(g, down.weight)
-        del g
-        if r is not None:
-            ctx.save_for_backward(r, w_norm)
-        else:
+        _hip.swiglu_fwd(h, u, h)
+        out = F.linear(h, down.weight)
+        del h, u
+        if r is None:
             ctx.save_for_backward(x2)
-        ctx.recompute_x = r is not None
-        ctx.eps, ctx.shape, ctx.dtype, ctx.layers = eps, shape, x.dtype, (gate, up, down)
+        else:
+            ctx.save_for_backward(r, w_norm)
+        ctx.from_residual, ctx.eps = r is not None, eps
+        ctx.shape, ctx.x_dtype, ctx.proj = shape, x.dtype, (gate, up, down)
         return out.view(*shape[:-1], out.shape[-1])
 
     @staticmethod
@@ -315,146 +396,173 @@ class _RecomputeMLP(torch.autograd.Function):
     def backward(ctx, dout):
         from . import _hip
 
-        gate, up, down = ctx.layers
-        if ctx.recompute_x:
+        gate, up, down = ctx.proj
+        if ctx.from_residual:
             from .norm_rope import rmsnorm_recompute
 
             r, w_norm = ctx.saved_tensors
-            x2 = rmsnorm_recompute(r.reshape(-1, r.shape[-1]), w_norm, ctx.eps, ctx.dtype)
+            x2 = rmsnorm_recompute(r.reshape(-1, r.shape[-1]), w_norm, ctx.eps, ctx.x_dtype)
         else:
             (x2,) = ctx.saved_tensors
         dh = torch.matmul(dout.reshape(-1, dout.shape[-1]), down.weight)
         g = F.linear(x2, gate.weight).contiguous()
         u = F.linear(x2, up.weight).contiguous()
         del x2
-        dh = dh.to(g.dtype).contiguous()
-        _hip.swiglu_bwd(dh, g, u, g, u)  # dg into g, du into u
+        _hip.swiglu_bwd(dh.to(g.dtype).contiguous(), g, u, g, u)  # dg into g, du into u
         del dh
-        dx_gate = torch.matmul(g, gate.weight).to(ctx.dtype)
+        dx_gate = torch.matmul(g, gate.weight).to(ctx.x_dtype)
         del g
-        dx_up = torch.matmul(u, up.weight).to(ctx.dtype)
+        dx_up = torch.matmul(u, up.weight).to(ctx.x_dtype)
         return dx_gate.view(ctx.shape), dx_up.view(ctx.shape), None, None, None, None, None, None
 
 
 def _mlp(mlp, xs, norm=None, residual=None, eps=None, norm_saves_y=False):
-    """Qwen2MLP on the post-attention norm's two outputs (gate, up): each projection takes its
-    own copy, so the norm backward sums their input gradients (reference packed.py:676-693).
-    Frozen projections: _RecomputeMLP (x recomputed from the norm's residual when the norm did
-    not save its output). Otherwise, with the kernels on, the projections as the model's modules
-    and silu(g) * u on the HIP kernel; else HF's ops."""
+    """The layer's MLP on the post-attention norm's output (reference packed.py:676-693). xs is
+    a tensor or the pair (x_gate, x_up) of fan-out copies. Frozen plain projections:
+    _RecomputeMLP (x recomputed from the norm's fp32 residual when the norm did not save its
+    output: eps given and norm_saves_y False). A plain silu MLP otherwise: the model's
+    projections with the HIP SwiGLU (HF's silu with the kernels off), gate and up reading their
+    own copies. Anything else (hooks, another MLP class or activation): mlp(x_gate)."""
     x_gate, x_up = xs if isinstance(xs, tuple) else (xs, xs)
-    layers = _mlp_layers(mlp, x_gate)
-    if layers is not None:
-        r = w_norm = None
-        if (eps is not None and not norm_saves_y and residual is not None
-                and residual.dtype == torch.float32 and residual.is_contiguous()):
-            r, w_norm = residual, norm.weight.detach().to(torch.float32)
-        return _RecomputeMLP.apply(x_gate, x_up, r, w_norm, eps, *layers)
-    if USE_KERNELS and _plain_silu_mlp(mlp, x_gate):
+    projections = _mlp_layers(mlp, x_gate)
+    if projections is not None:
+        from_residual = (eps is not None and not norm_saves_y and residual is not None
+                         and residual.dtype == torch.float32 and residual.is_contiguous())
+        r = residual if from_residual else None
+        w_norm = norm.weight.detach().to(torch.float32) if from_residual else None
+        return _RecomputeMLP.apply(x_gate, x_up, r, w_norm, eps, *projections)
+    if not _plain_silu_mlp(mlp, x_gate):
+        return mlp(x_gate)  # its own forward (and hooks); the copy x_up gets no gradient
+    if USE_KERNELS:
         from ..swiglu import swiglu
 
         return mlp.down_proj(swiglu(mlp.gate_proj(x_gate), mlp.up_proj(x_up)))
     return mlp.down_proj(mlp.act_fn(mlp.gate_proj(x_gate)) * mlp.up_proj(x_up))
 
 
+# ----------------------------------------------------------------------------------------
+# one decoder layer and the patched forward
+# ----------------------------------------------------------------------------------------
 def _layer(layer, residual, delta, rope_in, lens):
-    """One Qwen2DecoderLayer on packed tokens (reference packed.py:696-724). Returns
-    (residual, delta) with the layer output residual + delta (the add is left pending so that it
-    fuses with the next norm)."""
+    """One Qwen2DecoderLayer on the packed tokens (reference packed.py:696-724). Returns
+    (residual, delta): the layer's output is residual + delta, the add left to the next norm.
+    The input norm's output goes to five consumers, each with its own copy: q, k and v
+    projections and the q and v LoRA terms (a copy nothing consumes gets no gradient)."""
     attn = layer.self_attn
-    residual, (x_q, x_k, x_v) = _add_norm(layer.input_layernorm, residual, delta, n_out=3,
-                                          save_output=NORM_SAVE_OUTPUT)
-    n = x_q.shape[1]
-    hd = attn.head_dim
-    q = attn.q_proj(x_q).view(1, n, -1, hd)
-    k = attn.k_proj(x_k).view(1, n, -1, hd)
-    v = attn.v_proj(x_v).view(1, n, -1, hd)
-    q, k = _rope(q, k, rope_in)
-    o = attn.o_proj(_attention(attn, q, k, v, lens))
-    norm = layer.post_attention_layernorm
-    residual, xs, eps = _add_norm(norm, residual, o, with_eps=True, n_out=2,
+    residual, (x_q, x_ql, x_k, x_v, x_vl) = _add_norm(layer.input_layernorm, residual, delta,
+                                                      n_out=5, save_output=NORM_SAVE_OUTPUT)
+    n_tok, head_dim = x_q.shape[1], attn.head_dim
+    q, q_term = _project_q(attn.q_proj, x_q, x_ql)
+    k = _project(attn.k_proj, x_k)
+    v = _project(attn.v_proj, x_v, x_vl)
+    q, k = _rope(q.view(1, n_tok, -1, head_dim), k.view(1, n_tok, -1, head_dim), rope_in, q_term)
+    o = attn.o_proj(_attention(attn, q, k, v.view(1, n_tok, -1, head_dim), lens))
+    post = layer.post_attention_layernorm
+    residual, xs, eps = _add_norm(post, residual, o, with_eps=True, n_out=2,
                                   save_output=NORM_SAVE_OUTPUT)
-    return residual, _mlp(layer.mlp, xs, norm, residual, eps, norm_saves_y=NORM_SAVE_OUTPUT)
+    return residual, _mlp(layer.mlp, xs, post, residual, eps, norm_saves_y=NORM_SAVE_OUTPUT)
 
 
 def _unsupported(model, input_ids, attention_mask, past_key_values, inputs_embeds, use_cache,
                  kwargs):
-    """None if the packed path applies, else a short reason (reference packed.py:736-771)."""
+    """None when the packed path takes this call, else the reason it does not (reference
+    packed.py:736-771)."""
     if not isinstance(model, torch.nn.Module) or not hasattr(model, "layers"):
         return "not a real model"
     config = getattr(model, "config", None)
     if config is None:
         return "no config"
-    if inputs_embeds is not None:
-        return "inputs_embeds"
-    if not isinstance(input_ids, torch.Tensor) or input_ids.dim() != 2 or not input_ids.is_cuda:
-        return "input_ids not 2D CUDA"
-    if not isinstance(attention_mask, torch.Tensor) or attention_mask.shape != input_ids.shape:
-        return "attention_mask missing or not 2D"
-    if past_key_values is not None:
-        return "past_key_values"
-    if use_cache is None:
-        use_cache = getattr(config, "use_cache", False)
-    if use_cache:
-        return "use_cache"
-    for key in kwargs:
-        if key not in _IGNORED_KWARGS:
-            return f"kwarg {key}"
+    checks = (
+        (inputs_embeds is not None, "inputs_embeds"),
+        (not (isinstance(input_ids, torch.Tensor) and input_ids.dim() == 2 and input_ids.is_cuda),
+         "input_ids not 2D CUDA"),
+        (not (isinstance(attention_mask, torch.Tensor)
+              and attention_mask.shape == getattr(input_ids, "shape", None)),
+         "attention_mask missing or not 2D"),
+        (past_key_values is not None, "past_key_values"),
+        (getattr(config, "use_cache", False) if use_cache is None else use_cache, "use_cache"),
+    )
+    for failed, reason in checks:
+        if failed:
+            return reason
+    extra = [key for key in kwargs if key not in _IGNORED_KWARGS]
+    if extra:
+        return f"kwarg {extra[0]}"
     for key in ("output_attentions", "output_hidden_states"):
         if kwargs.get(key, getattr(config, key, False)):
             return key
     if getattr(config, "_attn_implementation", None) != "sdpa":
         return "attn_implementation is not sdpa"
-    if any(t != "full_attention" for t in getattr(config, "layer_types", ["full_attention"])):
+    if any(kind != "full_attention" for kind in getattr(config, "layer_types", ["full_attention"])):
         return "sliding window layers"
-    if getattr(model, "gradient_checkpointing", False) and model.training:
+    if model.training and getattr(model, "gradient_checkpointing", False):
         return "gradient checkpointing"
-    for layer in model.layers[: config.num_hidden_layers]:
-        if _has_hooks(layer) or _has_hooks(layer.self_attn):
-            return "hooks on decoder layers"
+    if any(_has_hooks(lyr) or _has_hooks(lyr.self_attn)
+           for lyr in model.layers[: config.num_hidden_layers]):
+        return "hooks on decoder layers"
     return None
 
 
+class _Packing:
+    """Geometry of one padded [B, L] batch: the row lengths (the forward's one host sync), the
+    flat indices of the real tokens in row-major order (rows stay in order, so each row is one
+    slice of the packed stream) and their positions: the column index, which is HF's default
+    arange(L) per row also under left padding, or the caller's position_ids gathered
+    (reference packed.py:800-814)."""
+
+    def __init__(self, attention_mask, position_ids):
+        real = attention_mask.bool()
+        self.B, self.L = real.shape
+        self.lens = real.sum(1).tolist()
+        self.T = sum(self.lens)
+        self.index = torch.nonzero_static(real.reshape(-1), size=self.T).squeeze(1)
+        if position_ids is None:
+            pos = self.index % self.L
+        else:
+            pos = position_ids.expand(self.B, self.L).reshape(-1).index_select(0, self.index)
+        self.positions = pos.to(torch.int64).unsqueeze(0)
+
+    def gather(self, t):
+        """[B, L, ...] -> the packed [1, T, ...]."""
+        return t.reshape(self.B * self.L, *t.shape[2:]).index_select(0, self.index).unsqueeze(0)
+
+    def scatter(self, packed):
+        """The packed [1, T, H] back to [B, L, H] with zeros at the pads. The copy goes into a
+        fresh zero tensor in place (autograd records it; the gradient gathers back)."""
+        full = packed.new_zeros(self.B * self.L, packed.shape[-1])
+        full.index_copy_(0, self.index, packed.squeeze(0))
+        return full.view(self.B, self.L, -1)
+
+
 def packed_forward(model, input_ids, attention_mask, position_ids, kwargs):
-    """The packed decoder (reference packed.py:800-840). Returns [B, L, H] hidden states, or None
-    for a batch with an empty row (the caller then runs the original forward)."""
-    B, L = input_ids.shape
-    mask = attention_mask.bool()
-    lens = mask.sum(1).tolist()  # the one host sync of the forward
-    if min(lens) == 0:
+    """The packed decoder body (reference packed.py:800-840): [B, L, H] hidden states, or None
+    when a row has no token (the caller then runs the original forward)."""
+    pack = _Packing(attention_mask, position_ids)
+    if min(pack.lens) == 0:
         return None
-    T = sum(lens)
-    flat_mask = mask.reshape(-1)
-    idx = torch.nonzero_static(flat_mask, size=T).squeeze(1)  # row-major: rows stay in order
-
-    if position_ids is None:
-        pos = idx % L  # HF default: arange(L) for every row (left padding keeps it)
-    else:
-        pos = position_ids.expand(B, L).reshape(-1).index_select(0, idx)
-    pos = pos.to(torch.int64).unsqueeze(0)
-
-    hidden = model.embed_tokens(input_ids.reshape(-1).index_select(0, idx).unsqueeze(0))
-    _WHERE[0], _WHERE[1] = bool(model.training), "embedding"
-    rope_in = _RopeInputs(model, hidden, pos)
-
+    hidden = model.embed_tokens(pack.gather(input_ids))
+    _Report.training, _Report.where = bool(model.training), "embedding"
+    emb_w = getattr(model.embed_tokens, "weight", None)
+    if (hidden.dtype != torch.float32 and isinstance(emb_w, torch.Tensor)
+            and emb_w.dtype == torch.float32):
+        _fallback("fp32 residual stream", f"embedding output is {hidden.dtype}")
+    rope_in = _RopeInputs(model, hidden, pack.positions)
     residual, delta = hidden, None
-    for i, layer in enumerate(model.layers[: model.config.num_hidden_layers]):
-        _WHERE[1] = i
-        residual, delta = _layer(layer, residual, delta, rope_in, lens)
-    _WHERE[1] = "final norm"
-    _, out = _add_norm(model.norm, residual, delta, final=True)
-    _WHERE[0] = False
-
-    # In place into fresh zeros (autograd records the copy; the source grad is
-    # grad.index_select(0, idx)).
-    full = out.new_zeros(B * L, out.shape[-1])
-    full.index_copy_(0, idx, out.squeeze(0))
-    return full.view(B, L, -1)
+    try:
+        for i, layer in enumerate(model.layers[: model.config.num_hidden_layers]):
+            _Report.where = i
+            residual, delta = _layer(layer, residual, delta, rope_in, pack.lens)
+        _Report.where = "final norm"
+        _, out = _add_norm(model.norm, residual, delta, final=True)
+    finally:
+        _Report.training = False
+    return pack.scatter(out)
 
 
 def patch():
-    """Class-patch Qwen2Model.forward (idempotent; the original stays at forward.__wrapped__).
-    Reference packed.py:843-875."""
+    """Replace Qwen2Model.forward by the packed decoder (idempotent). The original forward
+    stays at forward.__wrapped__ and serves every call the packed path does not take
+    (reference packed.py:843-875)."""
     from transformers.modeling_outputs import BaseModelOutputWithPast
     from transformers.models.qwen2 import modeling_qwen2
 
@@ -463,6 +571,7 @@ def patch():
         return
     original = cls.forward
 
+    @functools.wraps(original)
     def forward(self, input_ids=None, attention_mask=None, position_ids=None,
                 past_key_values=None, inputs_embeds=None, use_cache=None, **kwargs):
         reason = _unsupported(self, input_ids, attention_mask, past_key_values, inputs_embeds,
@@ -470,32 +579,30 @@ def patch():
         hidden = None
         if reason is None:
             hidden = packed_forward(self, input_ids, attention_mask, position_ids, kwargs)
-            if hidden is None:
-                reason = "a row without tokens"
-        if hidden is not None and getattr(self, "training", False):
-            _note_active()
+            reason = None if hidden is not None else "a row without tokens"
+        training = getattr(self, "training", False)
         if hidden is None:
-            if getattr(self, "training", False) and reason != "not a real model":
+            if training and reason != "not a real model":
                 _warn_once(reason)
             return original(self, input_ids=input_ids, attention_mask=attention_mask,
                             position_ids=position_ids, past_key_values=past_key_values,
                             inputs_embeds=inputs_embeds, use_cache=use_cache, **kwargs)
-        out = BaseModelOutputWithPast(last_hidden_state=hidden, past_key_values=None)
+        if training:
+            _note_active()
+        result = BaseModelOutputWithPast(last_hidden_state=hidden, past_key_values=None)
         return_dict = kwargs.get("return_dict", getattr(self.config, "return_dict", True))
-        return out.to_tuple() if return_dict is False else out
+        return result.to_tuple() if return_dict is False else result
 
     forward._solution_body_packed = True
-    forward.__wrapped__ = original
     cls.forward = forward
 
 
 @contextlib.contextmanager
 def kernels_enabled(on):
-    """Temporarily set USE_KERNELS (tests, benchmarks)."""
+    """USE_KERNELS set to `on` for the duration of the block (tests, benchmarks)."""
     global USE_KERNELS
-    old = USE_KERNELS
-    USE_KERNELS = on
+    saved, USE_KERNELS = USE_KERNELS, on
     try:
         yield
     finally:
-        USE_KERNELS = old
+        USE_KERNELS = saved
