@@ -295,12 +295,14 @@ def add_rmsnorm(r_in, delta, weight, eps=1e-6, out_dtype=torch.float16, n_out=1,
     """
     if out_dtype not in _FLOATS:
         raise TypeError(f"out_dtype {out_dtype} not supported")
-    slots, k = None, 0
-    if save_output and delta is not None and out_dtype in (torch.float16, torch.bfloat16):
-        slots, k = special_channels(weight)
+    # y stands in for the residual in backward only where it is worth it and well defined: a
+    # residual add happened and y is a 16-bit copy (else the fp32 r_out is saved)
+    keep_y = save_output and delta is not None and out_dtype != torch.float32
+    slots, n_exact = special_channels(weight) if keep_y else (None, 0)
     w = _weight_f32(weight, _wants_weight_grad(weight))
-    out = AddRMSNorm.apply(r_in, delta, w, float(eps), out_dtype, int(n_out), slots, k)
-    return (out[0], out[1]) if n_out == 1 else (out[0], tuple(out[1:]))
+    r_out, *ys = AddRMSNorm.apply(r_in, delta, w, float(eps), out_dtype, int(n_out), slots,
+                                  n_exact)
+    return r_out, (ys[0] if n_out == 1 else tuple(ys))
 
 
 def rmsnorm_recompute(r, w, eps, out_dtype=torch.float16):
@@ -309,10 +311,10 @@ def rmsnorm_recompute(r, w, eps, out_dtype=torch.float16):
     The same forward kernel as add_rmsnorm on its saved fp32 residual: bit-for-bit the y that
     add_rmsnorm returned for it. Reference: norm_rope.py:309-323.
     """
-    rows, n = r.shape
-    y = torch.empty((rows, n), device=r.device, dtype=out_dtype)
-    if rows > 0:
-        _hip.rmsnorm_fwd(r, w.detach().to(torch.float32).contiguous(), y, eps)
+    y = torch.empty(r.shape, device=r.device, dtype=out_dtype)
+    if r.shape[0]:
+        w32 = w.detach().to(torch.float32).contiguous()
+        _hip.rmsnorm_fwd(r, w32, y, eps)  # no rstd, no residual add: the forward's y only
     return y
 
 
