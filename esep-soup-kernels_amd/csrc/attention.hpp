@@ -147,11 +147,12 @@ __device__ __forceinline__ V ld_tr(const T* M, int r0, int c0, int lane) {
 // that the compiler does not track it: its own LDS-DMA tracking cannot tell the two buffers
 // apart for the transposing reads and would wait for the next tile before reading this one.
 // The kernel waits for the DMA itself (s_waitcnt vmcnt(0) before the barrier that publishes a
-// tile). M0 is written right before the load that reads it; the compiler sets M0 afresh before
-// each of its own uses (in the compiled attention kernels the asm's writes are its only ones).
+// tile). The LDS address goes in M0 through the "{m0}" operand constraint: the compiler itself
+// loads M0 before the instruction and knows what M0 holds afterwards (the asm only reads it),
+// so no M0 value of the compiler's own is ever overwritten behind its back.
 __device__ __forceinline__ void lds_dma_dword(const void* g, const void* lds) {
   const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dword %0, off" ::"v"(g), "s"(m) : "memory");
+  asm volatile("global_load_lds_dword %0, off" ::"v"(g), "{m0}"(m) : "memory");
 }
 
 // s_waitcnt vmcnt(0) (expcnt, lgkmcnt left at their maxima): through the builtin, so that the
