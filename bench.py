@@ -944,6 +944,96 @@ def kernel_rooflines(body, reps):
     return out
 
 
+def _cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def _cpu_time(fn, budget_s, min_reps=5):
+    """Median wall time of fn() over at least min_reps runs (after one warm-up), stopping at
+    budget_s or 20 runs."""
+    fn()
+    times = []
+    t_start = time.perf_counter()
+    while len(times) < min_reps or (time.perf_counter() - t_start < budget_s and len(times) < 20):
+        t0 = time.perf_counter()
+        fn()
+        times.append(time.perf_counter() - t0)
+    return statistics.median(times), len(times)
+
+
+def cpu_configs(cfg5, budget_s=2.0):
+    """The same PyTorch-eager fp32 HF path on the host cores for configs 1-3 (whole) and config
+    5 (its longest-sequence share: one 4096-token sequence at H = 3584, 28/4 heads), forward +
+    autograd backward; GB/s with e = 4 (BASELINE.md's CPU rule)."""
+    import torch
+
+    from oracle import hf_eager
+
+    threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+    torch.set_num_threads(threads)
+    g = torch.Generator().manual_seed(0)
+    eps, theta, D = 1e-6, 1e6, 128
+
+    def inv(d):
+        return 1.0 / (theta ** (torch.arange(0, d, 2, dtype=torch.float) / d))
+
+    def norm_pass(x, w, dy):
+        xr, wr = x.detach().requires_grad_(), w.detach().requires_grad_()
+        torch.autograd.grad(hf_eager.rms_norm(xr, wr, eps), [xr, wr], dy)
+
+    def rope_pass(q, k, dq, dk, pos):
+        qr, kr = q.detach().requires_grad_(), k.detach().requires_grad_()
+        cos, sin = hf_eager.rotary_cos_sin(inv(q.shape[-1]), pos, qr.dtype)
+        qe, ke = hf_eager.apply_rotary_pos_emb(qr, kr, cos, sin, unsqueeze_dim=1)
+        torch.autograd.grad([qe, ke], [qr, kr], [dq, dk])
+
+    def norm_case(T, H):
+        x, dy = torch.randn(T, H, generator=g), torch.randn(T, H, generator=g)
+        w = 1 + 0.02 * torch.randn(H, generator=g)
+        return lambda: norm_pass(x, w, dy)
+
+    def rope_case(B, S, HQ, HK, pos):
+        q, dq = torch.randn(B, HQ, S, D, generator=g), torch.randn(B, HQ, S, D, generator=g)
+        k, dk = torch.randn(B, HK, S, D, generator=g), torch.randn(B, HK, S, D, generator=g)
+        return lambda: rope_pass(q, k, dq, dk, pos)
+
+    e = 4
+    lens3 = torch.randint(64, 1025, (8,), generator=torch.Generator().manual_seed(0)).tolist()
+    T3 = sum(lens3)
+    pos3 = torch.cat([torch.arange(n) for n in lens3])[None, :]
+    c1 = norm_case(2048, 1536)
+    c2 = rope_case(4, 512, 12, 2, torch.arange(512).expand(4, 512))
+    c3n, c3r = norm_case(T3, 1536), rope_case(1, T3, 12, 2, pos3)
+    H5, HQ5, HK5 = cfg5["H"], cfg5["HQ"], cfg5["HK"]
+    c5n, c5r = norm_case(4096, H5), rope_case(1, 4096, HQ5, HK5, torch.arange(4096)[None, :])
+    nb = lambda T, H: norm_fwd_bytes(T, H, e, True) + norm_bwd_bytes(T, H, e, True)  # noqa: E731
+    cases = {
+        "config1": (c1, nb(2048, 1536), 2048, "the whole config"),
+        "config2": (c2, 2 * rope_bytes(2048, 12, 2, D, e), 2048, "the whole config"),
+        "config3": (lambda: (c3n(), c3r()), nb(T3, 1536) + 2 * rope_bytes(T3, 12, 2, D, e), T3,
+                    "the whole config"),
+        "config5": (lambda: (c5n(), c5n(), c5r()),
+                    2 * nb(4096, H5) + 2 * rope_bytes(4096, HQ5, HK5, D, e), 4096,
+                    "one 4096-token sequence of the 65536 (2 norms + q/k RoPE per token, as the "
+                    "GPU step)"),
+    }
+    out = {}
+    for name, (fn, nbytes, T, sample) in cases.items():
+        t, reps = _cpu_time(fn, budget_s)
+        out[name] = {"GB/s": round(nbytes / t / 1e9, 2), "tokens_per_s": round(T / t, 1),
+                     "ms": round(t * 1e3, 3), "reps": reps, "cores": threads,
+                     "cpu_model": _cpu_model(), "kind": "port", "sample": sample}
+        log(f"CPU {name}: {t * 1e3:.2f} ms ({out[name]['GB/s']} GB/s, {threads} threads)")
+    return out
+
+
 def cpu_baseline(cfg, budget_s=12.0, batch=2):
     """PyTorch-eager fp32 HF path (oracle/hf_eager.py) on the host cores: one layer of the
     workload (2 RMSNorms + q/k RoPE, forward + autograd backward) on `batch` of its 8 rows
@@ -954,15 +1044,7 @@ def cpu_baseline(cfg, budget_s=12.0, batch=2):
 
     threads = max(1, min(len(os.sched_getaffinity(0)), 16))
     torch.set_num_threads(threads)
-    model = "unknown"
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    model = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
+    model = _cpu_model()
     S, H, HQ, HK, D, eps = (cfg[k] for k in ("S", "H", "HQ", "HK", "D", "eps"))
     B = batch
     T = B * S
@@ -1109,6 +1191,11 @@ def main():
         log("CPU baseline (PyTorch eager fp32, one layer)")
         cpu = cpu_baseline(cfg)
         log(f"CPU: {cpu['value']} GB/s on {cpu['cores']} threads")
+        # the same eager path on the other configs, each beside its GPU figures
+        for name, row in cpu_configs(CFG5).items():
+            target = c5 if name == "config5" else small[name]
+            if target is not None:
+                target["cpu"] = row
 
     T = cfg["B"] * cfg["S"]
     out = {
