@@ -210,8 +210,25 @@ __global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd_dma(const AttnArgs
   const T* vbase = static_cast<const T*>(a.v) + (int64_t)kvh * D;
   const int ntiles = (kend - start + BN - 1) / BN;
 
-  // wavefront w moves rows w, w + 4, ... of the tile's K and V
+  // wavefront w moves rows w, w + 4, ... of the tile's K and V. A whole tile (the common case)
+  // walks the rows with scalar adds from the tile's row-w address; the last, partial tile
+  // clamps each row to kend - 1.
+  const int64_t k_step = 4 * a.k_rs, v_step = 4 * a.v_rs;  // elements between a wave's rows
+  const uint32_t voff = 4u * (uint32_t)lane;
   auto issue = [&](T* kd, T* vd, int kt) {
+    if (kt + BN <= kend) {
+      const T* kr = kbase + (int64_t)(kt + w) * a.k_rs;
+      const T* vr = vbase + (int64_t)(kt + w) * a.v_rs;
+#pragma unroll
+      for (int jj = 0; jj < BN / 4; ++jj) {
+        const int j = 4 * jj + w;
+        lds_dma_dword_s(kr, voff, kd + j * KP);
+        lds_dma_dword_s(vr, voff, vd + j * KP);
+        kr += k_step;
+        vr += v_step;
+      }
+      return;
+    }
 #pragma unroll
     for (int jj = 0; jj < BN / 4; ++jj) {
       const int j = 4 * jj + w;
