@@ -244,17 +244,33 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs 
   // DMA path: wavefront w moves rows w, w + NW, ... of Q and dO (one 256-byte row per
   // instruction) and wavefront 0 the lse / delta words (64 per instruction)
   const int wu = __builtin_amdgcn_readfirstlane(w);
+  const int64_t q_step = NW * a.q_rs, do_step = NW * b.do_rs;  // elements between a wave's rows
+  const uint32_t voff = 4u * (uint32_t)lane;
   auto issue = [&](int it, int buf) {
     const int h = h0 + it / nqt, qt = k0 + (it % nqt) * BQ;
     const int64_t col = (int64_t)h * D;
+    if (qt + BQ <= end) {
+      // a whole tile: the rows are walked with scalar adds from row qt + wu
+      const T* qr = static_cast<const T*>(a.q) + (int64_t)(qt + wu) * a.q_rs + col;
+      const T* dr = static_cast<const T*>(b.dout) + (int64_t)(qt + wu) * b.do_rs + col;
 #pragma unroll
-    for (int jj = 0; jj < BQ / NW; ++jj) {
-      const int j = NW * jj + wu;
-      const int r = qt + j < end ? qt + j : end - 1;
-      lds_dma_dword(reinterpret_cast<const uint32_t*>(static_cast<const T*>(a.q) + (int64_t)r * a.q_rs + col) + lane,
-                    &qs[buf][j * RP]);
-      lds_dma_dword(reinterpret_cast<const uint32_t*>(static_cast<const T*>(b.dout) + (int64_t)r * b.do_rs + col) + lane,
-                    &ds_[buf][j * RP]);
+      for (int jj = 0; jj < BQ / NW; ++jj) {
+        const int j = NW * jj + wu;
+        lds_dma_dword_s(qr, voff, &qs[buf][j * RP]);
+        lds_dma_dword_s(dr, voff, &ds_[buf][j * RP]);
+        qr += q_step;
+        dr += do_step;
+      }
+    } else {
+#pragma unroll
+      for (int jj = 0; jj < BQ / NW; ++jj) {
+        const int j = NW * jj + wu;
+        const int r = qt + j < end ? qt + j : end - 1;
+        lds_dma_dword(reinterpret_cast<const uint32_t*>(static_cast<const T*>(a.q) + (int64_t)r * a.q_rs + col) + lane,
+                      &qs[buf][j * RP]);
+        lds_dma_dword(reinterpret_cast<const uint32_t*>(static_cast<const T*>(b.dout) + (int64_t)r * b.do_rs + col) + lane,
+                      &ds_[buf][j * RP]);
+      }
     }
     if (wu == 0) {
 #pragma unroll
