@@ -32,6 +32,73 @@ namespace {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
+// One 32-key half of the dQ walk for a wavefront's 32 queries: keys kh .. kh + 31, held in rows
+// r0 .. r0 + 31 of the row-major LDS tiles ks / vs (pitch KP). S^T = K Q^T and dP^T = V dO^T
+// with the wave's Q and dO as B operands, dS^T = P^T * (dP^T - delta), then
+// dQ^T += K^T dS^T with K^T read transposed out of ks and dS^T in the permuted key order.
+template <typename T, int D, int KP>
+__device__ __forceinline__ void dq_half(const T* ks, const T* vs, int r0, int kh, int qw0, int qi,
+                                        int lane, float scale_log2, float lse2, float delta,
+                                        const typename Mfma<T>::v8 (&qb)[D / 16],
+                                        const typename Mfma<T>::v8 (&db)[D / 16],
+                                        f32x16 (&dqa)[D / 32]) {
+  using V8 = typename Mfma<T>::v8;
+  const int lq = lane & 31, hi = lane >> 5;
+  f32x16 s = f32x16{}, dp = f32x16{};
+  const T* krow = &ks[(r0 + lq) * KP + 8 * hi];
+  const T* vrow = &vs[(r0 + lq) * KP + 8 * hi];
+  // K and V operands read three ahead of the MFMAs (the scheduling barriers keep the
+  // compiler from sinking each read to just before its use; config 5 bwd 7.11 -> 6.97 ms
+  // together with the K^T operands below)
+  constexpr int KA = 3;
+  V8 kbuf[KA], vbuf[KA];
+#pragma unroll
+  for (int c = 0; c < KA; ++c) {
+    kbuf[c] = ld16<V8>(krow + 16 * c);
+    vbuf[c] = ld16<V8>(vrow + 16 * c);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int c = 0; c < D / 16; ++c) {
+    s = Mfma<T>::run(kbuf[c % KA], qb[c], s);
+    dp = Mfma<T>::run(vbuf[c % KA], db[c], dp);
+    if (c + KA < D / 16) {
+      kbuf[c % KA] = ld16<V8>(krow + 16 * (c + KA));
+      vbuf[c % KA] = ld16<V8>(vrow + 16 * (c + KA));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // the first two K^T operands of dQ (order j = 2 md + c2) read before the exponentials
+  constexpr int TA = 2;
+  V8 tbuf[TA];
+#pragma unroll
+  for (int j = 0; j < TA; ++j) tbuf[j] = ld_tr<V8, KP>(ks, r0 + 16 * (j % 2), 32 * (j / 2), lane);
+  __builtin_amdgcn_sched_barrier(0);
+  // the causal mask only bites on the half-tiles that reach past the wave's first query
+  if (kh + 31 > qw0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int kj = kh + 8 * (i / 4) + 4 * hi + (i % 4);
+      if (kj > qi) s[i] = -INFINITY;
+    }
+  }
+  V8 dsb[2];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float p = exp2_fast(fmaf(s[i], scale_log2, -lse2));
+    dsb[i / 8][i % 8] = (T)(p * (dp[i] - delta));
+  }
+  // dQ^T += K^T dS^T, keys in the permuted order of dsb, K^T read transposed out of ks
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < 2 * (D / 32); ++j) {
+    dqa[j / 2] = Mfma<T>::run(tbuf[j % TA], dsb[j % 2], dqa[j / 2]);
+    if (j + TA < 2 * (D / 32))
+      tbuf[j % TA] = ld_tr<V8, KP>(ks, r0 + 16 * ((j + TA) % 2), 32 * ((j + TA) / 2), lane);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // 2 wavefronts per SIMD without spills (unbounded, the compiler settles at 1).
 template <typename T, int D, int NW>
 __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq(const AttnBwdArgs b) {
@@ -105,61 +172,110 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq(const AttnBwdArgs b)
 
     // one 32-key half at a time (fewer live registers: 3 wavefronts per SIMD instead of 2)
 #pragma unroll
-    for (int sb = 0; sb < 2; ++sb) {
-      f32x16 s = f32x16{}, dp = f32x16{};
-      const T* krow = &ks[(32 * sb + lq) * KP + 8 * hi];
-      const T* vrow = &vs[(32 * sb + lq) * KP + 8 * hi];
-      // K and V operands read three ahead of the MFMAs (the scheduling barriers keep the
-      // compiler from sinking each read to just before its use; config 5 bwd 7.11 -> 6.97 ms
-      // together with the K^T operands below)
-      constexpr int KA = 3;
-      V8 kbuf[KA], vbuf[KA];
+    for (int sb = 0; sb < 2; ++sb)
+      dq_half<T, D, KP>(ks, vs, 32 * sb, kt + 32 * sb, qw0, qi, lane, a.scale_log2, lse2, delta,
+                        qb, db, dqa);
+  }
+  if (!qok) return;
+  store_rows_t<T, D>(static_cast<T*>(b.dq) + (int64_t)qi * b.dq_rs + (int64_t)h * D, dqa, hi,
+                     a.scale);
+}
+
+// dQ at D = 128 with the K / V tiles moved by LDS DMA, as the forward moves them: tiles of 32
+// keys through a ring of two buffers (tile t + 1 in flight while tile t is consumed, one barrier
+// per tile), whole tiles with scalar row addresses, the last partial tile with its rows clamped
+// to kend - 1 (finite data, always masked). Same prologue and per-half body as k_attn_bwd_dq.
+template <typename T, int NW>
+__global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq_dma(const AttnBwdArgs b) {
+  constexpr int D = 128;
+  constexpr int BN = 32;
+  using V8 = typename Mfma<T>::v8;
+  const AttnArgs& a = b.f;
+  constexpr int BM = 32 * NW;  // queries per block
+  constexpr int KP = D + kRowPad;
+  __shared__ __align__(16) T kv[2][2][BN * KP];  // [buffer][K, V][row-major tile]
+
+  const int seq = blockIdx.z, h = blockIdx.y;
+  int start, end;
+  seq_bounds(a.cu, seq, a.T, &start, &end);
+  const int ntiles_q = (end - start + BM - 1) / BM;
+  if ((int)blockIdx.x >= ntiles_q) return;
+  const int q0 = start + (ntiles_q - 1 - (int)blockIdx.x) * BM;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq = lane & 31, hi = lane >> 5;
+  const int kvh = h / (a.HQ / a.HK);
+  const int qw0 = q0 + 32 * w;
+  const int qi = qw0 + lq;
+  const bool qok = qi < end;
+  const bool wave_live = qw0 < end;
+  const int wq_last = qw0 + 31 < end ? qw0 + 31 : end - 1;
+
+  V8 qb[D / 16], db[D / 16];
+  float delta = 0.f;
+  {
+    const int64_t col = (int64_t)h * D + 8 * hi;
+    const T* qrow = static_cast<const T*>(a.q) + (int64_t)qi * a.q_rs + col;
+    const T* drow = static_cast<const T*>(b.dout) + (int64_t)qi * b.do_rs + col;
+    const T* orow = static_cast<const T*>(a.o) + (int64_t)qi * a.o_rs + col;
 #pragma unroll
-      for (int c = 0; c < KA; ++c) {
-        kbuf[c] = ld16<V8>(krow + 16 * c);
-        vbuf[c] = ld16<V8>(vrow + 16 * c);
-      }
-      __builtin_amdgcn_sched_barrier(0);
+    for (int c = 0; c < D / 16; ++c) {
+      qb[c] = qok ? ld16<V8>(qrow + 16 * c) : V8{};
+      db[c] = qok ? ld16<V8>(drow + 16 * c) : V8{};
+      const V8 o8 = qok ? ld16<V8>(orow + 16 * c) : V8{};
 #pragma unroll
-      for (int c = 0; c < D / 16; ++c) {
-        s = Mfma<T>::run(kbuf[c % KA], qb[c], s);
-        dp = Mfma<T>::run(vbuf[c % KA], db[c], dp);
-        if (c + KA < D / 16) {
-          kbuf[c % KA] = ld16<V8>(krow + 16 * (c + KA));
-          vbuf[c % KA] = ld16<V8>(vrow + 16 * (c + KA));
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      // the first two K^T operands of dQ (order j = 2 md + c2) read before the exponentials
-      constexpr int TA = 2;
-      V8 tbuf[TA];
-#pragma unroll
-      for (int j = 0; j < TA; ++j) tbuf[j] = ld_tr<V8, KP>(ks, 32 * sb + 16 * (j % 2), 32 * (j / 2), lane);
-      __builtin_amdgcn_sched_barrier(0);
-      // the causal mask only bites on the half-tiles that reach past the wave's first query
-      if (kt + 32 * sb + 31 > qw0) {
-#pragma unroll
-        for (int i = 0; i < 16; ++i) {
-          const int kj = kt + 32 * sb + 8 * (i / 4) + 4 * hi + (i % 4);
-          if (kj > qi) s[i] = -INFINITY;
-        }
-      }
-      V8 dsb[2];
-#pragma unroll
-      for (int i = 0; i < 16; ++i) {
-        const float p = exp2_fast(fmaf(s[i], a.scale_log2, -lse2));
-        dsb[i / 8][i % 8] = (T)(p * (dp[i] - delta));
-      }
-      // dQ^T += K^T dS^T, keys in the permuted order of dsb, K^T read transposed out of ks
-      __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-      for (int j = 0; j < 2 * (D / 32); ++j) {
-        dqa[j / 2] = Mfma<T>::run(tbuf[j % TA], dsb[j % 2], dqa[j / 2]);
-        if (j + TA < 2 * (D / 32))
-          tbuf[j % TA] = ld_tr<V8, KP>(ks, 32 * sb + 16 * ((j + TA) % 2), 32 * ((j + TA) / 2), lane);
-        __builtin_amdgcn_sched_barrier(0);
-      }
+      for (int e = 0; e < 8; ++e) delta = fmaf((float)db[c][e], (float)o8[e], delta);
     }
+    delta = pair_sum(delta);
+    if (qok && hi == 0) b.delta[(int64_t)h * a.T + qi] = delta;
+  }
+  const float lse2 = qok ? a.lse[(int64_t)h * a.T + qi] * kLog2e : 0.f;
+
+  f32x16 dqa[D / 32];
+#pragma unroll
+  for (int md = 0; md < D / 32; ++md) dqa[md] = f32x16{};
+  const int kend = end < q0 + BM ? end : q0 + BM;
+  const T* kbase = static_cast<const T*>(a.k) + (int64_t)kvh * D;
+  const T* vbase = static_cast<const T*>(a.v) + (int64_t)kvh * D;
+  const int ntiles = (kend - start + BN - 1) / BN;
+  const int64_t k_step = NW * a.k_rs, v_step = NW * a.v_rs;  // elements between a wave's rows
+  const uint32_t voff = 4u * (uint32_t)lane;
+
+  // wavefront w moves rows w, w + NW, ... of the tile's K and V
+  auto issue = [&](T* kd, T* vd, int kt) {
+    if (kt + BN <= kend) {
+      const T* kr = kbase + (int64_t)(kt + w) * a.k_rs;
+      const T* vr = vbase + (int64_t)(kt + w) * a.v_rs;
+#pragma unroll
+      for (int jj = 0; jj < BN / NW; ++jj) {
+        const int j = NW * jj + w;
+        lds_dma_dword_s(kr, voff, kd + j * KP);
+        lds_dma_dword_s(vr, voff, vd + j * KP);
+        kr += k_step;
+        vr += v_step;
+      }
+      return;
+    }
+#pragma unroll
+    for (int jj = 0; jj < BN / NW; ++jj) {
+      const int j = NW * jj + w;
+      const int r = kt + j < kend ? kt + j : kend - 1;
+      lds_dma_dword(reinterpret_cast<const uint32_t*>(kbase + (int64_t)r * a.k_rs) + lane, kd + j * KP);
+      lds_dma_dword(reinterpret_cast<const uint32_t*>(vbase + (int64_t)r * a.v_rs) + lane, vd + j * KP);
+    }
+  };
+
+  if (ntiles > 0) issue(kv[0][0], kv[0][1], start);
+  for (int t = 0; t < ntiles; ++t) {
+    // this wavefront's DMA of tile t has landed; the barrier publishes every wavefront's rows
+    // and certifies that tile t - 1, in the other buffer, is consumed
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __syncthreads();
+    if (t + 1 < ntiles) issue(kv[(t + 1) & 1][0], kv[(t + 1) & 1][1], start + (t + 1) * BN);
+    const int kt = start + t * BN;
+    if (!wave_live || kt > wq_last) continue;
+    dq_half<T, D, KP>(kv[t & 1][0], kv[t & 1][1], 0, kt, qw0, qi, lane, a.scale_log2, lse2, delta,
+                      qb, db, dqa);
   }
   if (!qok) return;
   store_rows_t<T, D>(static_cast<T*>(b.dq) + (int64_t)qi * b.dq_rs + (int64_t)h * D, dqa, hi,
@@ -421,7 +537,10 @@ hipError_t bwd_run(const AttnBwdArgs& b, int max_seqlen, hipStream_t s) {
   // block the early wavefronts idle through the later key tiles).
   constexpr int QW = 4;
   const dim3 gq((max_seqlen + 32 * QW - 1) / (32 * QW), b.f.HQ, b.f.n_seq);
-  hipLaunchKernelGGL((k_attn_bwd_dq<T, D, QW>), gq, dim3(64 * QW), 0, s, b);
+  if constexpr (D == 128)
+    hipLaunchKernelGGL((k_attn_bwd_dq_dma<T, QW>), gq, dim3(64 * QW), 0, s, b);
+  else
+    hipLaunchKernelGGL((k_attn_bwd_dq<T, D, QW>), gq, dim3(64 * QW), 0, s, b);
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   auto dkdv = [&](auto nw, auto bq) {
