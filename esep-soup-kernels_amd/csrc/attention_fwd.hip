@@ -260,11 +260,232 @@ __global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd_dma(const AttnArgs
     a.lse[(int64_t)h * a.T + qi] = (m + log2f(l)) * 0.69314718055994531f;
 }
 
+// ---------------------------------------------------------------------------------------
+// D = 128 forward on swizzled, unpadded LDS tiles moved 1 KiB per DMA instruction.
+//
+// A tile row is 256 bytes = 16 chunks of 16 bytes. Chunk c of tile row r sits at chunk
+// position c ^ f(r) of that row, f(r) = 4 (r & 3) + ((r >> 2) & 3): the 16 rows a K-operand read
+// touches (one chunk each) and the 4 rows x 4 chunks a transposing V read touches in one pass
+// land on 16 different chunk positions, so neither read has bank conflicts without a pitch pad.
+// global_load_lds_dwordx4 writes lane l's 16 bytes at M0 + 16 l (checked on the device), so one
+// instruction fills 4 whole rows: lane l loads the global chunk that belongs at its position,
+// ((l & 15) ^ f(row)) of row l >> 4 of its 4-row group. A 32-key tile of K and V is 16 such
+// instructions per block (4 per wavefront) instead of 64 row-sized ones, and 16 KiB of LDS
+// instead of 19.5.
+// ---------------------------------------------------------------------------------------
+
+__device__ __forceinline__ void lds_dma_x4_s(const void* base, uint32_t voff, const void* lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(m) : "memory");
+}
+__device__ __forceinline__ void lds_dma_x4(const void* g, const void* lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(m) : "memory");
+}
+
+// swizzled chunk position of chunk c in tile row r
+__device__ __forceinline__ int swz(int r) { return 4 * (r & 3) + ((r >> 2) & 3); }
+
+// One 32-key half (the whole 32-key tile) of the online softmax, as fwd_half, on swizzled tiles:
+// the K operand of chunk pair c is read at byte (256 lq + 16 ((2c + hi) ^ f(lq))) of the K tile,
+// the V^T operands of ld_tr's lane mapping at their rows' swizzled chunk positions.
+template <typename T>
+__device__ __forceinline__ void fwd_tile_swz(const char* ks, const char* vs, int kh, int qw0,
+                                             int qi, int lane, float scale_log2,
+                                             const typename Mfma<T>::v8 (&qb)[8],
+                                             f32x16 (&oacc)[4], float& m, float& l) {
+  using V8 = typename Mfma<T>::v8;
+  typedef __attribute__((address_space(3))) s16x4* lds_ptr;
+  const int lq = lane & 31, hi = lane >> 5;
+  f32x16 acc = f32x16{};
+  // K: byte offset of chunk (2c + hi) of row lq = k0 ^ (32 c)
+  const int fk = swz(lq);
+  const uint32_t k0 = 256u * lq + 16u * ((hi ^ fk) & 1) + 32u * (fk >> 1);
+  constexpr int KA = 3;
+  V8 kbuf[KA];
+#pragma unroll
+  for (int c = 0; c < KA; ++c) kbuf[c] = ld16<V8>(ks + (k0 ^ (32u * c)));
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    acc = Mfma<T>::run(kbuf[c % KA], qb[c], acc);
+    if (c + KA < 8) kbuf[c % KA] = ld16<V8>(ks + (k0 ^ (32u * (c + KA))));
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  // V^T operand j (rows 16 (j & 1) + 4 (g >> 1) + k (+ 8), columns 32 (j >> 1) + 16 (g & 1) + 4 m):
+  // byte offset ((v_u | 64 k) ^ 64 (j >> 1)) + 4096 (j & 1) for the lower (u = 0) and upper
+  // (u = 1) read, with v_u = 256 (4 (g >> 1) + k + 8 u) + 16 L_u + 8 (m & 1) and
+  // L_u = (2 (g & 1) + (m >> 1)) ^ (((g >> 1) + 2 u) & 3).
+  const int g = lane >> 4, kk = (lane >> 2) & 3, mm = lane & 3;
+  uint32_t vo[2];
+#pragma unroll
+  for (int u = 0; u < 2; ++u) {
+    const int L = (2 * (g & 1) + (mm >> 1)) ^ (((g >> 1) + 2 * u) & 3);
+    vo[u] = (256u * (4 * (g >> 1) + kk + 8 * u) + 16u * L + 8u * (mm & 1)) | (64u * kk);
+  }
+  auto ldv = [&](int j) {
+    const uint32_t x = 64u * (j >> 1), y = 4096u * (j & 1);
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr)(vs + ((vo[0] ^ x) + y)));
+    const s16x4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr)(vs + ((vo[1] ^ x) + y)));
+    return __builtin_bit_cast(V8, __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7));
+  };
+  constexpr int VA = 2;
+  V8 vbuf[VA];
+#pragma unroll
+  for (int j = 0; j < VA; ++j) vbuf[j] = ldv(j);
+  __builtin_amdgcn_sched_barrier(0);
+  if (kh + 31 > qw0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int kj = kh + 8 * (i / 4) + 4 * hi + (i % 4);
+      if (kj > qi) acc[i] = -INFINITY;
+    }
+  }
+  float mx = acc[0];
+#pragma unroll
+  for (int i = 1; i < 16; ++i) mx = fmaxf(mx, acc[i]);
+  mx = pair_max(mx) * scale_log2;
+  const bool grow = mx > m + 8.f;
+  float alpha = 1.f;
+  if (grow) {
+    alpha = exp2_fast(m - mx);
+    m = mx;
+  }
+  const float nm = m == -INFINITY ? 0.f : -m;
+  float ps = 0.f;
+  V8 pb[2];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float p = exp2_fast(fmaf(acc[i], scale_log2, nm));
+    ps += p;
+    pb[i / 8][i % 8] = (T)p;
+  }
+  ps = pair_sum(ps);
+  l = fmaf(l, alpha, ps);
+  if (__any(grow)) {
+#pragma unroll
+    for (int md = 0; md < 4; ++md) oacc[md] *= alpha;
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    oacc[j / 2] = Mfma<T>::run(vbuf[j % VA], pb[j % 2], oacc[j / 2]);
+    if (j + VA < 8) vbuf[j % VA] = ldv(j + VA);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
+// The D = 128 forward kernel: blocks, queries and the online softmax as k_attn_fwd_dma; the
+// 32-key K / V tiles go through a ring of NBUF swizzled buffers (tile t + NBUF - 1 in flight
+// while tile t is consumed).
+template <typename T, int NBUF>
+__global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd_swz(const AttnArgs a) {
+  constexpr int D = 128;
+  constexpr int BN = 32;
+  constexpr int TILE = BN * 256;  // bytes of one K or V tile
+  using V8 = typename Mfma<T>::v8;
+  __shared__ __align__(1024) char kv[NBUF][2][TILE];  // [buffer][K, V][swizzled rows]
+
+  const int seq = blockIdx.z, h = blockIdx.y;
+  int start, end;
+  seq_bounds(a.cu, seq, a.T, &start, &end);
+  const int ntiles_q = (end - start + kAttnBM - 1) / kAttnBM;
+  if ((int)blockIdx.x >= ntiles_q) return;
+  const int q0 = start + (ntiles_q - 1 - (int)blockIdx.x) * kAttnBM;  // heaviest tiles first
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lq = lane & 31, hi = lane >> 5;
+  const int kvh = h / (a.HQ / a.HK);
+  const int qw0 = q0 + 32 * w;
+  const int qi = qw0 + lq;
+  const bool wave_live = qw0 < end;
+  const int wq_last = qw0 + 31 < end ? qw0 + 31 : end - 1;
+
+  V8 qb[D / 16];
+  {
+    const T* qrow = static_cast<const T*>(a.q) + (int64_t)qi * a.q_rs + (int64_t)h * D + 8 * hi;
+#pragma unroll
+    for (int c = 0; c < D / 16; ++c)
+      qb[c] = qi < end ? ld16<V8>(qrow + 16 * c) : V8{};
+  }
+
+  f32x16 oacc[D / 32];
+#pragma unroll
+  for (int md = 0; md < D / 32; ++md) oacc[md] = f32x16{};
+  float m = -INFINITY, l = 0.f;
+  const int kend = end < q0 + kAttnBM ? end : q0 + kAttnBM;
+  const char* kbase = reinterpret_cast<const char*>(static_cast<const T*>(a.k) + (int64_t)kvh * D);
+  const char* vbase = reinterpret_cast<const char*>(static_cast<const T*>(a.v) + (int64_t)kvh * D);
+  const int64_t krs = a.k_rs * (int64_t)sizeof(T), vrs = a.v_rs * (int64_t)sizeof(T);  // bytes
+  const int ntiles = (kend - start + BN - 1) / BN;
+
+  // Wavefront w fills row groups w and w + 4 (rows 4q .. 4q + 3, q & 3 = w) of K and of V.
+  // Lane l: row (l >> 4) of the group, the global chunk for position l & 15.
+  const int lrow = lane >> 4;
+  const int lchunk = (lane & 15) ^ (4 * lrow + w);
+  const uint32_t kvoff = (uint32_t)(lrow * krs) + 16u * lchunk;
+  const uint32_t vvoff = (uint32_t)(lrow * vrs) + 16u * lchunk;
+  auto issue = [&](int buf, int kt) {
+    char* kd = kv[buf][0];
+    char* vd = kv[buf][1];
+    if (kt + BN <= kend) {
+#pragma unroll
+      for (int qq = 0; qq < 2; ++qq) {
+        const int q = w + 4 * qq;
+        lds_dma_x4_s(kbase + (int64_t)(kt + 4 * q) * krs, kvoff, kd + 1024 * q);
+        lds_dma_x4_s(vbase + (int64_t)(kt + 4 * q) * vrs, vvoff, vd + 1024 * q);
+      }
+      return;
+    }
+    // the last, partial tile: rows past kend repeat row kend - 1 (finite data, always masked)
+#pragma unroll
+    for (int qq = 0; qq < 2; ++qq) {
+      const int q = w + 4 * qq;
+      const int r0 = kt + 4 * q + lrow;
+      const int r = r0 < kend ? r0 : kend - 1;
+      lds_dma_x4(kbase + (int64_t)r * krs + 16 * lchunk, kd + 1024 * q);
+      lds_dma_x4(vbase + (int64_t)r * vrs + 16 * lchunk, vd + 1024 * q);
+    }
+  };
+
+#pragma unroll
+  for (int p = 0; p < NBUF - 1; ++p)
+    if (p < ntiles) issue(p, start + p * BN);
+  for (int t = 0; t < ntiles; ++t) {
+    // this wavefront's DMA of tile t has landed (its later tiles, 4 instructions each, may
+    // still be in flight); the barrier publishes every wavefront's rows and certifies that
+    // tile t - 1 is consumed, freeing its buffer for tile t + NBUF - 1
+    const int later = (ntiles - 1 - t) < (NBUF - 2) ? (ntiles - 1 - t) : (NBUF - 2);
+    if (later >= 2)
+      __builtin_amdgcn_s_waitcnt(kWaitVm0 + 8);
+    else if (later == 1)
+      __builtin_amdgcn_s_waitcnt(kWaitVm0 + 4);
+    else
+      __builtin_amdgcn_s_waitcnt(kWaitVm0);
+    __syncthreads();
+    if (t + NBUF - 1 < ntiles) issue((t + NBUF - 1) % NBUF, start + (t + NBUF - 1) * BN);
+    const int kt = start + t * BN;
+    if (!wave_live || kt > wq_last) continue;
+    fwd_tile_swz<T>(kv[t % NBUF][0], kv[t % NBUF][1], kt, qw0, qi, lane, a.scale_log2, qb, oacc,
+                    m, l);
+  }
+
+  if (!wave_live || qi >= end) return;
+  store_rows_t<T, D>(static_cast<T*>(a.o) + (int64_t)qi * a.o_rs + (int64_t)h * D, oacc, hi,
+                     l > 0.f ? 1.f / l : 0.f);
+  if (hi == 0 && a.lse != nullptr)
+    a.lse[(int64_t)h * a.T + qi] = (m + log2f(l)) * 0.69314718055994531f;
+}
+
+#ifndef ESEP_FWD_NBUF
+#define ESEP_FWD_NBUF 2
+#endif
+
 template <typename T>
 hipError_t fwd_d(const AttnArgs& a, int D, dim3 grid, hipStream_t s, bool* sup) {
   *sup = true;
   if (D == 128)
-    hipLaunchKernelGGL((k_attn_fwd_dma<T>), grid, dim3(kAttnThreads), 0, s, a);
+    hipLaunchKernelGGL((k_attn_fwd_swz<T, ESEP_FWD_NBUF>), grid, dim3(kAttnThreads), 0, s, a);
   else if (D == 64)
     hipLaunchKernelGGL((k_attn_fwd<T, 64>), grid, dim3(kAttnThreads), 0, s, a);
   else {
