@@ -167,6 +167,20 @@ __device__ __forceinline__ void lds_dma_dword_s(const void* base, uint32_t voff,
 // compiler's own wait tracking sees it too.
 constexpr int kWaitVm0 = 0x0F70;
 
+// XCD-aware block order. The hardware deals the workgroups of a launch round-robin over the 8
+// XCDs (workgroup b to XCD b % 8), each with its own L2. A kernel that wants the C blocks of one
+// group (e.g. all query tiles of one (sequence, head): they read the same K / V rows) on one
+// XCD launches xcd_grid(C, groups) one-dimensional blocks and maps its workgroup id through
+// xcd_order: XCD x then takes groups x, x + 8, x + 16, ... whole, so every XCD still gets a mix
+// of groups (sequences of different lengths). The result is the block's index in the
+// group-major order (group * C + index in the group); indices past C * groups (the padding to a
+// multiple of 8 groups) belong to no group and their blocks exit.
+__device__ __forceinline__ int xcd_order(int b, int C) {
+  const int xcd = b % 8, slot = b / 8;
+  return (xcd + 8 * (slot / C)) * C + slot % C;
+}
+inline int64_t xcd_grid(int64_t C, int64_t groups) { return (groups + 7) / 8 * 8 * C; }
+
 // Sequence s's token range [start, end), clamped into [0, T].
 __device__ __forceinline__ void seq_bounds(const int32_t* cu, int s, int64_t T, int* start,
                                            int* end) {

@@ -186,7 +186,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq(const AttnBwdArgs b)
 // per tile), whole tiles with scalar row addresses, the last partial tile with its rows clamped
 // to kend - 1 (finite data, always masked). Same prologue and per-half body as k_attn_bwd_dq.
 template <typename T, int NW>
-__global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq_dma(const AttnBwdArgs b) {
+__global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq_dma(const AttnBwdArgs b, int qtiles) {
   constexpr int D = 128;
   constexpr int BN = 32;
   using V8 = typename Mfma<T>::v8;
@@ -195,12 +195,16 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq_dma(const AttnBwdArg
   constexpr int KP = D + kRowPad;
   __shared__ __align__(16) T kv[2][2][BN * KP];  // [buffer][K, V][row-major tile]
 
-  const int seq = blockIdx.z, h = blockIdx.y;
+  // XCD-aware order: the query tiles of one (sequence, head) run on one XCD
+  const int lin = xcd_order((int)blockIdx.x, qtiles);
+  const int bx = lin % qtiles, rest = lin / qtiles;
+  const int h = rest % a.HQ, seq = rest / a.HQ;
+  if (seq >= a.n_seq) return;
   int start, end;
   seq_bounds(a.cu, seq, a.T, &start, &end);
   const int ntiles_q = (end - start + BM - 1) / BM;
-  if ((int)blockIdx.x >= ntiles_q) return;
-  const int q0 = start + (ntiles_q - 1 - (int)blockIdx.x) * BM;
+  if (bx >= ntiles_q) return;
+  const int q0 = start + (ntiles_q - 1 - bx) * BM;
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane & 31, hi = lane >> 5;
@@ -289,7 +293,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq_dma(const AttnBwdArg
 // at config 5 the backward takes 8.4 ms with 4 and 10.8 ms with 8, at config 4 0.30 vs 0.28 ms.
 // D = 64 takes 4 wavefronts and 64-query tiles.
 template <typename T, int D, int NW, int BQ>
-__global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs b) {
+__global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs b, int ktiles) {
   constexpr int NT = 64 * NW, BK = 32 * NW;
   using V8 = typename Mfma<T>::v8;
   const AttnArgs& a = b.f;
@@ -305,14 +309,19 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs 
   __shared__ __align__(16) float ld_s[NB][2 * BQ];  // lse (log2 units without DMA), then delta
   __shared__ __align__(16) T vsm[BK * RP];  // this block's V rows (B operands of dP)
 
-  const int seq = blockIdx.z;
+  // XCD-aware order: the key tiles of one (sequence, kv head, part) run on one XCD (they read
+  // the same Q / dO rows)
   const int split = b.split;                 // query-head groups per kv head
-  const int kh = blockIdx.y / split, part = blockIdx.y % split;
+  const int lin = xcd_order((int)blockIdx.x, ktiles);
+  const int bx = lin % ktiles, rest = lin / ktiles;
+  const int yy = rest % (a.HK * split), seq = rest / (a.HK * split);
+  if (seq >= a.n_seq) return;
+  const int kh = yy / split, part = yy % split;
   int start, end;
   seq_bounds(a.cu, seq, a.T, &start, &end);
   const int ntiles = (end - start + BK - 1) / BK;
-  if ((int)blockIdx.x >= ntiles) return;
-  const int k0 = start + (int)blockIdx.x * BK;  // early key tiles see the most queries
+  if (bx >= ntiles) return;
+  const int k0 = start + bx * BK;  // early key tiles see the most queries
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int lq = lane & 31, hi = lane >> 5;
   const int kw0 = k0 + 32 * w;  // this wavefront's first key
@@ -537,16 +546,27 @@ hipError_t bwd_run(const AttnBwdArgs& b, int max_seqlen, hipStream_t s) {
   // block the early wavefronts idle through the later key tiles).
   constexpr int QW = 4;
   const dim3 gq((max_seqlen + 32 * QW - 1) / (32 * QW), b.f.HQ, b.f.n_seq);
-  if constexpr (D == 128)
-    hipLaunchKernelGGL((k_attn_bwd_dq_dma<T, QW>), gq, dim3(64 * QW), 0, s, b);
-  else
+  if constexpr (D == 128) {
+    const int64_t n = xcd_grid(gq.x, (int64_t)gq.y * gq.z);
+    if (n > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((k_attn_bwd_dq_dma<T, QW>), dim3((unsigned)n), dim3(64 * QW), 0, s, b,
+                       (int)gq.x);
+  } else {
     hipLaunchKernelGGL((k_attn_bwd_dq<T, D, QW>), gq, dim3(64 * QW), 0, s, b);
+  }
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
+  bool too_big = false;
   auto dkdv = [&](auto nw, auto bq) {
     constexpr int NW = decltype(nw)::value, BQ = decltype(bq)::value;
-    const dim3 gk((max_seqlen + 32 * NW - 1) / (32 * NW), b.f.HK * b.split, b.f.n_seq);
-    hipLaunchKernelGGL((k_attn_bwd_dkdv<T, D, NW, BQ>), gk, dim3(64 * NW), 0, s, b);
+    const int64_t ktiles = (max_seqlen + 32 * NW - 1) / (32 * NW);
+    const int64_t n = xcd_grid(ktiles, (int64_t)b.f.HK * b.split * b.f.n_seq);
+    if (n > 0x7fffffff) {
+      too_big = true;
+      return;
+    }
+    hipLaunchKernelGGL((k_attn_bwd_dkdv<T, D, NW, BQ>), dim3((unsigned)n), dim3(64 * NW), 0, s, b,
+                       (int)ktiles);
   };
   if constexpr (D == 128) {
     if (b.split > 1)
@@ -556,6 +576,7 @@ hipError_t bwd_run(const AttnBwdArgs& b, int max_seqlen, hipStream_t s) {
   } else {
     dkdv(std::integral_constant<int, 4>{}, std::integral_constant<int, 64>{});
   }
+  if (too_big) return hipErrorInvalidValue;
   e = hipGetLastError();
   if (e != hipSuccess || b.split == 1) return e;
   const int64_t quads = b.f.T * b.f.HK * D / 4;

@@ -379,19 +379,23 @@ __device__ __forceinline__ void fwd_tile_swz(const char* ks, const char* vs, int
 // 32-key K / V tiles go through a ring of NBUF swizzled buffers (tile t + NBUF - 1 in flight
 // while tile t is consumed).
 template <typename T, int NBUF>
-__global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd_swz(const AttnArgs a) {
+__global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd_swz(const AttnArgs a, int qtiles) {
   constexpr int D = 128;
   constexpr int BN = 32;
   constexpr int TILE = BN * 256;  // bytes of one K or V tile
   using V8 = typename Mfma<T>::v8;
   __shared__ __align__(1024) char kv[NBUF][2][TILE];  // [buffer][K, V][swizzled rows]
 
-  const int seq = blockIdx.z, h = blockIdx.y;
+  // XCD-aware order (xcd_order): the query tiles of one (sequence, head) run on one XCD.
+  const int lin = xcd_order((int)blockIdx.x, qtiles);
+  const int bx = lin % qtiles, rest = lin / qtiles;
+  const int h = rest % a.HQ, seq = rest / a.HQ;
+  if (seq >= a.n_seq) return;
   int start, end;
   seq_bounds(a.cu, seq, a.T, &start, &end);
   const int ntiles_q = (end - start + kAttnBM - 1) / kAttnBM;
-  if ((int)blockIdx.x >= ntiles_q) return;
-  const int q0 = start + (ntiles_q - 1 - (int)blockIdx.x) * kAttnBM;  // heaviest tiles first
+  if (bx >= ntiles_q) return;
+  const int q0 = start + (ntiles_q - 1 - bx) * kAttnBM;  // heaviest tiles first
   const int tid = threadIdx.x, lane = tid & 63;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lq = lane & 31, hi = lane >> 5;
@@ -477,15 +481,15 @@ __global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd_swz(const AttnArgs
     a.lse[(int64_t)h * a.T + qi] = (m + log2f(l)) * 0.69314718055994531f;
 }
 
-#ifndef ESEP_FWD_NBUF
-#define ESEP_FWD_NBUF 2
-#endif
-
 template <typename T>
 hipError_t fwd_d(const AttnArgs& a, int D, dim3 grid, hipStream_t s, bool* sup) {
   *sup = true;
-  if (D == 128)
-    hipLaunchKernelGGL((k_attn_fwd_swz<T, ESEP_FWD_NBUF>), grid, dim3(kAttnThreads), 0, s, a);
+  if (D == 128) {
+    const int64_t n = xcd_grid(grid.x, (int64_t)grid.y * grid.z);
+    if (n > 0x7fffffff) return hipErrorInvalidValue;
+    hipLaunchKernelGGL((k_attn_fwd_swz<T, 2>), dim3((unsigned)n), dim3(kAttnThreads), 0, s, a,
+                       (int)grid.x);
+  }
   else if (D == 64)
     hipLaunchKernelGGL((k_attn_fwd<T, 64>), grid, dim3(kAttnThreads), 0, s, a);
   else {
