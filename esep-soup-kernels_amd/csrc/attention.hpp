@@ -167,6 +167,109 @@ __device__ __forceinline__ void lds_dma_dword_s(const void* base, uint32_t voff,
 // compiler's own wait tracking sees it too.
 constexpr int kWaitVm0 = 0x0F70;
 
+// ---------------------------------------------------------------------------------------
+// Swizzled, unpadded LDS tiles of 256-byte token rows (D = 128, 16-bit elements), filled 1 KiB
+// per DMA instruction.
+//
+// Chunk c (16 bytes) of tile row r sits at chunk position c ^ swz(r), swz(r) = 4 (r & 3) +
+// ((r >> 2) & 3): the 16 rows a row-operand read touches (one chunk each, SwzRow) and the
+// 4 rows x 4 chunks a transposing read touches in one pass (SwzTr) land on 16 different
+// positions, so neither read has bank conflicts without a pitch pad (checked on the CPU).
+// global_load_lds_dwordx4 writes lane l's 16 bytes at M0 + 16 l (checked on the device), so one
+// instruction fills 4 whole rows: lane l loads the global chunk that belongs at its position,
+// ((l & 15) ^ swz(row)) of row l >> 4 of its 4-row group.
+// ---------------------------------------------------------------------------------------
+__device__ __forceinline__ void lds_dma_x4_s(const void* base, uint32_t voff, const void* lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(m) : "memory");
+}
+__device__ __forceinline__ void lds_dma_x4(const void* g, const void* lds) {
+  const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
+  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(m) : "memory");
+}
+
+__device__ __forceinline__ int swz(int r) { return 4 * (r & 3) + ((r >> 2) & 3); }
+
+// One wavefront's share of filling a ROWS-row swizzled tile from token rows r0 .. r0 + ROWS - 1
+// of a tensor (base: row 0's first element of the head; rs: bytes between token rows): with
+// NW wavefronts (a multiple of 4), wavefront w fills the 4-row groups w, w + NW, ... Rows at or
+// past rend repeat row rend - 1. A whole tile is addressed from an SGPR base; a partial one
+// clamps each lane's row.
+template <int ROWS, int NW>
+struct SwzFill {
+  static_assert(NW % 4 == 0 && ROWS % (4 * NW) == 0, "groups per wavefront");
+  int w, lrow, lchunk;
+  int64_t rs;
+  uint32_t voff;
+  __device__ __forceinline__ SwzFill(int lane, int w_, int64_t rs_) : w(w_), rs(rs_) {
+    lrow = lane >> 4;
+    lchunk = (lane & 15) ^ (4 * lrow + (w & 3));  // swz(4 q + lrow) with q & 3 = w & 3
+    voff = (uint32_t)(lrow * rs) + 16u * (uint32_t)lchunk;
+  }
+  __device__ __forceinline__ void whole(char* dst, const char* base, int r0) const {
+#pragma unroll
+    for (int i = 0; i < ROWS / (4 * NW); ++i) {
+      const int q = w + NW * i;
+      lds_dma_x4_s(base + (int64_t)(r0 + 4 * q) * rs, voff, dst + 1024 * q);
+    }
+  }
+  __device__ __forceinline__ void partial(char* dst, const char* base, int r0, int rend) const {
+#pragma unroll
+    for (int i = 0; i < ROWS / (4 * NW); ++i) {
+      const int q = w + NW * i;
+      const int r = r0 + 4 * q + lrow < rend ? r0 + 4 * q + lrow : rend - 1;
+      lds_dma_x4(base + (int64_t)r * rs + 16 * lchunk, dst + 1024 * q);
+    }
+  }
+};
+
+// Two tiles of the same rows (e.g. K and V) with one whole-or-partial decision.
+template <int ROWS, int NW>
+__device__ __forceinline__ void swz_fill2(const SwzFill<ROWS, NW>& fa, char* da, const char* ba,
+                                          const SwzFill<ROWS, NW>& fb, char* db, const char* bb,
+                                          int r0, int rend) {
+  if (r0 + ROWS <= rend) {
+    fa.whole(da, ba, r0);
+    fb.whole(db, bb, r0);
+  } else {
+    fa.partial(da, ba, r0, rend);
+    fb.partial(db, bb, r0, rend);
+  }
+}
+
+// Row operand (A or B of v_mfma_f32_32x32x16 with the rows in lanes): lane (lq, hi) reads
+// chunk 2c + hi of tile row lq (+ 32 h for rows 32 h + lq) at byte
+// (swz_row_base(lane) ^ 32 c) + 8192 h.
+__device__ __forceinline__ uint32_t swz_row_base(int lane) {
+  const int lq = lane & 31, hi = lane >> 5, f = swz(lq);
+  return 256u * lq + 16u * ((hi ^ f) & 1) + 32u * (f >> 1);
+}
+
+// Transposing operand read (ld_tr's lane mapping) out of a swizzled tile: rows rb + 4 (g >> 1)
+// + k (+ 8), columns 32 md + 16 (g & 1) + 4 m, for rb a multiple of 16. Byte offset
+// ((o_u | 64 k) ^ 64 md) + 256 rb for the lower (u = 0) and upper (u = 1) read, with
+// o_u = 256 (4 (g >> 1) + k + 8 u) + 16 L_u + 8 (m & 1) and
+// L_u = (2 (g & 1) + (m >> 1)) ^ (((g >> 1) + 2 u) & 3).
+struct SwzTr {
+  uint32_t o[2];
+  __device__ __forceinline__ explicit SwzTr(int lane) {
+    const int g = lane >> 4, k = (lane >> 2) & 3, m = lane & 3;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int L = (2 * (g & 1) + (m >> 1)) ^ (((g >> 1) + 2 * u) & 3);
+      o[u] = (256u * (4 * (g >> 1) + k + 8 * u) + 16u * L + 8u * (m & 1)) | (64u * k);
+    }
+  }
+  template <typename V>
+  __device__ __forceinline__ V read(const char* tile, int rb, int md) const {
+    typedef __attribute__((address_space(3))) s16x4* lds_ptr;
+    const uint32_t x = 64u * md, y = 256u * rb;
+    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr)(tile + ((o[0] ^ x) + y)));
+    const s16x4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr)(tile + ((o[1] ^ x) + y)));
+    return __builtin_bit_cast(V, __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7));
+  }
+};
+
 // XCD-aware block order. The hardware deals the workgroups of a launch round-robin over the 8
 // XCDs (workgroup b to XCD b % 8), each with its own L2. A kernel that wants the C blocks of one
 // group (e.g. all query tiles of one (sequence, head): they read the same K / V rows) on one

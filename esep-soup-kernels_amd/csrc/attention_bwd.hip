@@ -99,6 +99,64 @@ __device__ __forceinline__ void dq_half(const T* ks, const T* vs, int r0, int kh
   }
 }
 
+// dq_half on swizzled 32-row tiles (attention.hpp: SwzFill, swz_row_base, SwzTr): the K and V
+// row operands at (swz_row_base ^ 32 c), the K^T operands through SwzTr.
+template <typename T>
+__device__ __forceinline__ void dq_tile_swz(const char* ks, const char* vs, int kh, int qw0, int qi,
+                                            int lane, float scale_log2, float lse2, float delta,
+                                            const typename Mfma<T>::v8 (&qb)[8],
+                                            const typename Mfma<T>::v8 (&db)[8],
+                                            f32x16 (&dqa)[4]) {
+  using V8 = typename Mfma<T>::v8;
+  const int hi = lane >> 5;
+  f32x16 s = f32x16{}, dp = f32x16{};
+  const uint32_t r0 = swz_row_base(lane);
+  constexpr int KA = 3;
+  V8 kbuf[KA], vbuf[KA];
+#pragma unroll
+  for (int c = 0; c < KA; ++c) {
+    kbuf[c] = ld16<V8>(ks + (r0 ^ (32u * c)));
+    vbuf[c] = ld16<V8>(vs + (r0 ^ (32u * c)));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int c = 0; c < 8; ++c) {
+    s = Mfma<T>::run(kbuf[c % KA], qb[c], s);
+    dp = Mfma<T>::run(vbuf[c % KA], db[c], dp);
+    if (c + KA < 8) {
+      kbuf[c % KA] = ld16<V8>(ks + (r0 ^ (32u * (c + KA))));
+      vbuf[c % KA] = ld16<V8>(vs + (r0 ^ (32u * (c + KA))));
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  }
+  const SwzTr kt(lane);
+  constexpr int TA = 2;
+  V8 tbuf[TA];
+#pragma unroll
+  for (int j = 0; j < TA; ++j) tbuf[j] = kt.template read<V8>(ks, 16 * (j & 1), j >> 1);
+  __builtin_amdgcn_sched_barrier(0);
+  if (kh + 31 > qw0) {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const int kj = kh + 8 * (i / 4) + 4 * hi + (i % 4);
+      if (kj > qi) s[i] = -INFINITY;
+    }
+  }
+  V8 dsb[2];
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float p = exp2_fast(fmaf(s[i], scale_log2, -lse2));
+    dsb[i / 8][i % 8] = (T)(p * (dp[i] - delta));
+  }
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    dqa[j / 2] = Mfma<T>::run(tbuf[j % TA], dsb[j % 2], dqa[j / 2]);
+    if (j + TA < 8) tbuf[j % TA] = kt.template read<V8>(ks, 16 * ((j + TA) & 1), (j + TA) >> 1);
+    __builtin_amdgcn_sched_barrier(0);
+  }
+}
+
 // 2 wavefronts per SIMD without spills (unbounded, the compiler settles at 1).
 template <typename T, int D, int NW>
 __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq(const AttnBwdArgs b) {
@@ -181,10 +239,10 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq(const AttnBwdArgs b)
                      a.scale);
 }
 
-// dQ at D = 128 with the K / V tiles moved by LDS DMA, as the forward moves them: tiles of 32
-// keys through a ring of two buffers (tile t + 1 in flight while tile t is consumed, one barrier
-// per tile), whole tiles with scalar row addresses, the last partial tile with its rows clamped
-// to kend - 1 (finite data, always masked). Same prologue and per-half body as k_attn_bwd_dq.
+// dQ at D = 128 with the K / V tiles moved as the forward moves them: swizzled 32-key tiles
+// filled by dwordx4 LDS DMA through a ring of two buffers (tile t + 1 in flight while tile t is
+// consumed, one barrier per tile). Same prologue as k_attn_bwd_dq; dq_tile_swz is dq_half on
+// the swizzled tiles.
 template <typename T, int NW>
 __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq_dma(const AttnBwdArgs b, int qtiles) {
   constexpr int D = 128;
@@ -192,8 +250,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq_dma(const AttnBwdArg
   using V8 = typename Mfma<T>::v8;
   const AttnArgs& a = b.f;
   constexpr int BM = 32 * NW;  // queries per block
-  constexpr int KP = D + kRowPad;
-  __shared__ __align__(16) T kv[2][2][BN * KP];  // [buffer][K, V][row-major tile]
+  __shared__ __align__(1024) char kv[2][2][BN * 256];  // [buffer][K, V][swizzled tile]
 
   // XCD-aware order: the query tiles of one (sequence, head) run on one XCD
   const int lin = xcd_order((int)blockIdx.x, qtiles);
@@ -239,35 +296,14 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq_dma(const AttnBwdArg
 #pragma unroll
   for (int md = 0; md < D / 32; ++md) dqa[md] = f32x16{};
   const int kend = end < q0 + BM ? end : q0 + BM;
-  const T* kbase = static_cast<const T*>(a.k) + (int64_t)kvh * D;
-  const T* vbase = static_cast<const T*>(a.v) + (int64_t)kvh * D;
+  const char* kbase = reinterpret_cast<const char*>(static_cast<const T*>(a.k) + (int64_t)kvh * D);
+  const char* vbase = reinterpret_cast<const char*>(static_cast<const T*>(a.v) + (int64_t)kvh * D);
   const int ntiles = (kend - start + BN - 1) / BN;
-  const int64_t k_step = NW * a.k_rs, v_step = NW * a.v_rs;  // elements between a wave's rows
-  const uint32_t voff = 4u * (uint32_t)lane;
-
-  // wavefront w moves rows w, w + NW, ... of the tile's K and V
-  auto issue = [&](T* kd, T* vd, int kt) {
-    if (kt + BN <= kend) {
-      const T* kr = kbase + (int64_t)(kt + w) * a.k_rs;
-      const T* vr = vbase + (int64_t)(kt + w) * a.v_rs;
-#pragma unroll
-      for (int jj = 0; jj < BN / NW; ++jj) {
-        const int j = NW * jj + w;
-        lds_dma_dword_s(kr, voff, kd + j * KP);
-        lds_dma_dword_s(vr, voff, vd + j * KP);
-        kr += k_step;
-        vr += v_step;
-      }
-      return;
-    }
-#pragma unroll
-    for (int jj = 0; jj < BN / NW; ++jj) {
-      const int j = NW * jj + w;
-      const int r = kt + j < kend ? kt + j : kend - 1;
-      lds_dma_dword(reinterpret_cast<const uint32_t*>(kbase + (int64_t)r * a.k_rs) + lane, kd + j * KP);
-      lds_dma_dword(reinterpret_cast<const uint32_t*>(vbase + (int64_t)r * a.v_rs) + lane, vd + j * KP);
-    }
-  };
+  // wavefront w fills row groups w and w + NW of the K and V tiles (rows past kend repeat row
+  // kend - 1: finite data, always masked)
+  const SwzFill<BN, NW> fk(lane, w, a.k_rs * (int64_t)sizeof(T));
+  const SwzFill<BN, NW> fv(lane, w, a.v_rs * (int64_t)sizeof(T));
+  auto issue = [&](char* kd, char* vd, int kt) { swz_fill2(fk, kd, kbase, fv, vd, vbase, kt, kend); };
 
   if (ntiles > 0) issue(kv[0][0], kv[0][1], start);
   for (int t = 0; t < ntiles; ++t) {
@@ -278,8 +314,8 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq_dma(const AttnBwdArg
     if (t + 1 < ntiles) issue(kv[(t + 1) & 1][0], kv[(t + 1) & 1][1], start + (t + 1) * BN);
     const int kt = start + t * BN;
     if (!wave_live || kt > wq_last) continue;
-    dq_half<T, D, KP>(kv[t & 1][0], kv[t & 1][1], 0, kt, qw0, qi, lane, a.scale_log2, lse2, delta,
-                      qb, db, dqa);
+    dq_tile_swz<T>(kv[t & 1][0], kv[t & 1][1], kt, qw0, qi, lane, a.scale_log2, lse2, delta, qb,
+                   db, dqa);
   }
   if (!qok) return;
   store_rows_t<T, D>(static_cast<T*>(b.dq) + (int64_t)qi * b.dq_rs + (int64_t)h * D, dqa, hi,

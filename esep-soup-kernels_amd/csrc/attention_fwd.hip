@@ -260,32 +260,9 @@ __global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd_dma(const AttnArgs
     a.lse[(int64_t)h * a.T + qi] = (m + log2f(l)) * 0.69314718055994531f;
 }
 
-// ---------------------------------------------------------------------------------------
-// D = 128 forward on swizzled, unpadded LDS tiles moved 1 KiB per DMA instruction.
+// D = 128 forward on swizzled, unpadded LDS tiles (the layout, its DMA and its readers are in
+// attention.hpp: swz, SwzFill, swz_row_base, SwzTr).
 //
-// A tile row is 256 bytes = 16 chunks of 16 bytes. Chunk c of tile row r sits at chunk
-// position c ^ f(r) of that row, f(r) = 4 (r & 3) + ((r >> 2) & 3): the 16 rows a K-operand read
-// touches (one chunk each) and the 4 rows x 4 chunks a transposing V read touches in one pass
-// land on 16 different chunk positions, so neither read has bank conflicts without a pitch pad.
-// global_load_lds_dwordx4 writes lane l's 16 bytes at M0 + 16 l (checked on the device), so one
-// instruction fills 4 whole rows: lane l loads the global chunk that belongs at its position,
-// ((l & 15) ^ f(row)) of row l >> 4 of its 4-row group. A 32-key tile of K and V is 16 such
-// instructions per block (4 per wavefront) instead of 64 row-sized ones, and 16 KiB of LDS
-// instead of 19.5.
-// ---------------------------------------------------------------------------------------
-
-__device__ __forceinline__ void lds_dma_x4_s(const void* base, uint32_t voff, const void* lds) {
-  const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-  asm volatile("global_load_lds_dwordx4 %0, %1" ::"v"(voff), "s"(base), "{m0}"(m) : "memory");
-}
-__device__ __forceinline__ void lds_dma_x4(const void* g, const void* lds) {
-  const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-  asm volatile("global_load_lds_dwordx4 %0, off" ::"v"(g), "{m0}"(m) : "memory");
-}
-
-// swizzled chunk position of chunk c in tile row r
-__device__ __forceinline__ int swz(int r) { return 4 * (r & 3) + ((r >> 2) & 3); }
-
 // One 32-key half (the whole 32-key tile) of the online softmax, as fwd_half, on swizzled tiles:
 // the K operand of chunk pair c is read at byte (256 lq + 16 ((2c + hi) ^ f(lq))) of the K tile,
 // the V^T operands of ld_tr's lane mapping at their rows' swizzled chunk positions.
@@ -295,12 +272,9 @@ __device__ __forceinline__ void fwd_tile_swz(const char* ks, const char* vs, int
                                              const typename Mfma<T>::v8 (&qb)[8],
                                              f32x16 (&oacc)[4], float& m, float& l) {
   using V8 = typename Mfma<T>::v8;
-  typedef __attribute__((address_space(3))) s16x4* lds_ptr;
   const int lq = lane & 31, hi = lane >> 5;
   f32x16 acc = f32x16{};
-  // K: byte offset of chunk (2c + hi) of row lq = k0 ^ (32 c)
-  const int fk = swz(lq);
-  const uint32_t k0 = 256u * lq + 16u * ((hi ^ fk) & 1) + 32u * (fk >> 1);
+  const uint32_t k0 = swz_row_base(lane);
   constexpr int KA = 3;
   V8 kbuf[KA];
 #pragma unroll
@@ -312,23 +286,9 @@ __device__ __forceinline__ void fwd_tile_swz(const char* ks, const char* vs, int
     if (c + KA < 8) kbuf[c % KA] = ld16<V8>(ks + (k0 ^ (32u * (c + KA))));
     __builtin_amdgcn_sched_barrier(0);
   }
-  // V^T operand j (rows 16 (j & 1) + 4 (g >> 1) + k (+ 8), columns 32 (j >> 1) + 16 (g & 1) + 4 m):
-  // byte offset ((v_u | 64 k) ^ 64 (j >> 1)) + 4096 (j & 1) for the lower (u = 0) and upper
-  // (u = 1) read, with v_u = 256 (4 (g >> 1) + k + 8 u) + 16 L_u + 8 (m & 1) and
-  // L_u = (2 (g & 1) + (m >> 1)) ^ (((g >> 1) + 2 u) & 3).
-  const int g = lane >> 4, kk = (lane >> 2) & 3, mm = lane & 3;
-  uint32_t vo[2];
-#pragma unroll
-  for (int u = 0; u < 2; ++u) {
-    const int L = (2 * (g & 1) + (mm >> 1)) ^ (((g >> 1) + 2 * u) & 3);
-    vo[u] = (256u * (4 * (g >> 1) + kk + 8 * u) + 16u * L + 8u * (mm & 1)) | (64u * kk);
-  }
-  auto ldv = [&](int j) {
-    const uint32_t x = 64u * (j >> 1), y = 4096u * (j & 1);
-    const s16x4 lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr)(vs + ((vo[0] ^ x) + y)));
-    const s16x4 up = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_ptr)(vs + ((vo[1] ^ x) + y)));
-    return __builtin_bit_cast(V8, __builtin_shufflevector(lo, up, 0, 1, 2, 3, 4, 5, 6, 7));
-  };
+  // V^T operand j: rows 16 (j & 1) .., columns 32 (j >> 1) .. of the V tile
+  const SwzTr vt(lane);
+  auto ldv = [&](int j) { return vt.template read<V8>(vs, 16 * (j & 1), j >> 1); };
   constexpr int VA = 2;
   V8 vbuf[VA];
 #pragma unroll
@@ -423,33 +383,11 @@ __global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd_swz(const AttnArgs
   const int64_t krs = a.k_rs * (int64_t)sizeof(T), vrs = a.v_rs * (int64_t)sizeof(T);  // bytes
   const int ntiles = (kend - start + BN - 1) / BN;
 
-  // Wavefront w fills row groups w and w + 4 (rows 4q .. 4q + 3, q & 3 = w) of K and of V.
-  // Lane l: row (l >> 4) of the group, the global chunk for position l & 15.
-  const int lrow = lane >> 4;
-  const int lchunk = (lane & 15) ^ (4 * lrow + w);
-  const uint32_t kvoff = (uint32_t)(lrow * krs) + 16u * lchunk;
-  const uint32_t vvoff = (uint32_t)(lrow * vrs) + 16u * lchunk;
+  // Wavefront w fills row groups w and w + 4 of the K and V tiles (rows past kend repeat row
+  // kend - 1: finite data, always masked).
+  const SwzFill<BN, 4> fk(lane, w, krs), fv(lane, w, vrs);
   auto issue = [&](int buf, int kt) {
-    char* kd = kv[buf][0];
-    char* vd = kv[buf][1];
-    if (kt + BN <= kend) {
-#pragma unroll
-      for (int qq = 0; qq < 2; ++qq) {
-        const int q = w + 4 * qq;
-        lds_dma_x4_s(kbase + (int64_t)(kt + 4 * q) * krs, kvoff, kd + 1024 * q);
-        lds_dma_x4_s(vbase + (int64_t)(kt + 4 * q) * vrs, vvoff, vd + 1024 * q);
-      }
-      return;
-    }
-    // the last, partial tile: rows past kend repeat row kend - 1 (finite data, always masked)
-#pragma unroll
-    for (int qq = 0; qq < 2; ++qq) {
-      const int q = w + 4 * qq;
-      const int r0 = kt + 4 * q + lrow;
-      const int r = r0 < kend ? r0 : kend - 1;
-      lds_dma_x4(kbase + (int64_t)r * krs + 16 * lchunk, kd + 1024 * q);
-      lds_dma_x4(vbase + (int64_t)r * vrs + 16 * lchunk, vd + 1024 * q);
-    }
+    swz_fill2(fk, kv[buf][0], kbase, fv, kv[buf][1], vbase, kt, kend);
   };
 
 #pragma unroll
