@@ -323,7 +323,22 @@ struct TileRows {
       *reinterpret_cast<uint4*>(&dst[(idx % ROWS) * P + 8 * (idx / ROWS)]) = r[j];
     }
   }
+
+  // the same rows into a swizzled, unpadded tile (256-byte rows: D = 128 of 16-bit elements;
+  // chunk c of row r at position c ^ swz(r))
+  __device__ __forceinline__ void store_swz(char* dst, int tid) const;
 };
+
+template <typename T, int D, int ROWS, int NT>
+__device__ __forceinline__ void TileRows<T, D, ROWS, NT>::store_swz(char* dst, int tid) const {
+  static_assert(D * sizeof(T) == 256, "swizzled tiles have 256-byte rows");
+#pragma unroll
+  for (int j = 0; j < N; ++j) {
+    const int idx = tid + NT * j;
+    const int row = idx % ROWS, chunk = idx / ROWS;
+    *reinterpret_cast<uint4*>(dst + 256 * row + 16 * (chunk ^ swz(row))) = r[j];
+  }
+}
 
 // Store a wavefront's [32 tokens x D] result held transposed in MFMA accumulators (acc[md]
 // element 4 j + e is column 32 md + 8 j + 4 hi + e of token `row`), times `mul`.

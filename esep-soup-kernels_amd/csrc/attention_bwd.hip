@@ -338,12 +338,15 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs 
   // buffers, item it + 1 in flight while item it is consumed, one barrier per item; query rows
   // past the sequence end repeat its last row and are masked (p = 0). Otherwise (D = 64: rows of
   // 128 bytes) they move through registers, the next item prefetched, rows past the end zeroed.
+  // With DMA the tiles are swizzled and unpadded (attention.hpp: SwzFill, swz_row_base, SwzTr;
+  // 256-byte rows), otherwise row-major with pitch RP.
   constexpr bool DMA = D == 128;
   constexpr int NB = DMA ? 2 : 1;
-  __shared__ __align__(16) T qs[NB][BQ * RP];   // Q row-major (A operand of S; transposed, of dK^T)
-  __shared__ __align__(16) T ds_[NB][BQ * RP];  // dO row-major (A operand of dP; transposed, of dV^T)
+  constexpr int ROWB = DMA ? 256 : RP * (int)sizeof(T);  // bytes per tile row
+  __shared__ __align__(1024) char qs[NB][BQ * ROWB];   // Q (A operand of S; transposed, of dK^T)
+  __shared__ __align__(1024) char ds_[NB][BQ * ROWB];  // dO (A operand of dP; transposed, of dV^T)
   __shared__ __align__(16) float ld_s[NB][2 * BQ];  // lse (log2 units without DMA), then delta
-  __shared__ __align__(16) T vsm[BK * RP];  // this block's V rows (B operands of dP)
+  __shared__ __align__(1024) char vsm[BK * ROWB];  // this block's V rows (B operands of dP)
 
   // XCD-aware order: the key tiles of one (sequence, kv head, part) run on one XCD (they read
   // the same Q / dO rows)
@@ -378,9 +381,17 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs 
   {
     TileRows<T, D, BK, NT> vr;
     vr.load(static_cast<const T*>(a.v) + (int64_t)kh * D, a.v_rs, k0, end, tid);
-    vr.template store<RP>(vsm, tid);
+    if constexpr (DMA)
+      vr.store_swz(vsm, tid);
+    else
+      vr.template store<RP>(reinterpret_cast<T*>(vsm), tid);
   }
-  const T* vlds = &vsm[(32 * w + lq) * RP + 8 * hi];
+  // row-operand reads of this wave's V rows (32 w + lq) and of the Q / dO tiles' rows
+  // (32 qh + lq): chunk pair c at byte rop + rowc(c) of the row group's base
+  const uint32_t rop = DMA ? swz_row_base(lane) : (uint32_t)(lq * RP * (int)sizeof(T) + 16 * hi);
+  auto rowc = [&](int c) -> uint32_t { return DMA ? (rop ^ (32u * c)) : rop + 32u * c; };
+  const char* vlds = vsm + 32 * w * ROWB;
+  const SwzTr trd(lane);
   f32x16 dka[D / 32], dva[D / 32];
 #pragma unroll
   for (int md = 0; md < D / 32; ++md) dka[md] = dva[md] = f32x16{};
@@ -405,34 +416,15 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs 
   // DMA path: wavefront w moves rows w, w + NW, ... of Q and dO (one 256-byte row per
   // instruction) and wavefront 0 the lse / delta words (64 per instruction)
   const int wu = __builtin_amdgcn_readfirstlane(w);
-  const int64_t q_step = NW * a.q_rs, do_step = NW * b.do_rs;  // elements between a wave's rows
-  const uint32_t voff = 4u * (uint32_t)lane;
+  // DMA path: wavefront w fills row groups w, w + NW, ... of the swizzled Q and dO tiles (rows
+  // past the sequence end repeat its last row) and wavefront 0 the lse / delta words
+  const SwzFill<BQ, NW> fq(lane, wu, a.q_rs * (int64_t)sizeof(T));
+  const SwzFill<BQ, NW> fd(lane, wu, b.do_rs * (int64_t)sizeof(T));
   auto issue = [&](int it, int buf) {
     const int h = h0 + it / nqt, qt = k0 + (it % nqt) * BQ;
     const int64_t col = (int64_t)h * D;
-    if (qt + BQ <= end) {
-      // a whole tile: the rows are walked with scalar adds from row qt + wu
-      const T* qr = static_cast<const T*>(a.q) + (int64_t)(qt + wu) * a.q_rs + col;
-      const T* dr = static_cast<const T*>(b.dout) + (int64_t)(qt + wu) * b.do_rs + col;
-#pragma unroll
-      for (int jj = 0; jj < BQ / NW; ++jj) {
-        const int j = NW * jj + wu;
-        lds_dma_dword_s(qr, voff, &qs[buf][j * RP]);
-        lds_dma_dword_s(dr, voff, &ds_[buf][j * RP]);
-        qr += q_step;
-        dr += do_step;
-      }
-    } else {
-#pragma unroll
-      for (int jj = 0; jj < BQ / NW; ++jj) {
-        const int j = NW * jj + wu;
-        const int r = qt + j < end ? qt + j : end - 1;
-        lds_dma_dword(reinterpret_cast<const uint32_t*>(static_cast<const T*>(a.q) + (int64_t)r * a.q_rs + col) + lane,
-                      &qs[buf][j * RP]);
-        lds_dma_dword(reinterpret_cast<const uint32_t*>(static_cast<const T*>(b.dout) + (int64_t)r * b.do_rs + col) + lane,
-                      &ds_[buf][j * RP]);
-      }
-    }
+    swz_fill2(fq, qs[buf], reinterpret_cast<const char*>(static_cast<const T*>(a.q) + col), fd,
+              ds_[buf], reinterpret_cast<const char*>(static_cast<const T*>(b.dout) + col), qt, end);
     if (wu == 0) {
 #pragma unroll
       for (int k = 0; k < 2 * BQ / 64; ++k) {
@@ -462,8 +454,8 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs 
       if (it + 1 < items) issue(it + 1, buf ^ 1);
     } else {
       __syncthreads();  // the previous item's LDS reads are done
-      pq.template store<RP>(qs[0], tid);
-      pd.template store<RP>(ds_[0], tid);
+      pq.template store<RP>(reinterpret_cast<T*>(qs[0]), tid);
+      pd.template store<RP>(reinterpret_cast<T*>(ds_[0]), tid);
       if (tid < BQ) {
         ld_s[0][tid] = lse_n;
         ld_s[0][BQ + tid] = del_n;
@@ -473,8 +465,8 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs 
     }
     // every query of the tile comes before this wave's keys: nothing to add
     if (!wave_live || qt + BQ - 1 < kw0) continue;
-    const T* qsb = qs[buf];
-    const T* dsb = ds_[buf];
+    const char* qsb = qs[buf];
+    const char* dsb = ds_[buf];
     const float* lse_s = ld_s[buf];
     const float* del_s = ld_s[buf] + BQ;
     // with DMA, rows past the sequence end hold repeated data: mask them like future queries
@@ -485,12 +477,12 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs 
 #pragma unroll
     for (int qh = 0; qh < BQ / 32; ++qh) {
       f32x16 s = f32x16{}, dp = f32x16{};
-      const T* qrow = &qsb[(32 * qh + lq) * RP + 8 * hi];
-      const T* drow = &dsb[(32 * qh + lq) * RP + 8 * hi];
+      const char* qrow = qsb + 32 * qh * ROWB;
+      const char* drow = dsb + 32 * qh * ROWB;
 #pragma unroll
       for (int c = 0; c < D / 16; ++c) {
-        s = Mfma<T>::run(ld16<V8>(qrow + 16 * c), kb[c], s);
-        dp = Mfma<T>::run(ld16<V8>(drow + 16 * c), ld16<V8>(vlds + 16 * c), dp);
+        s = Mfma<T>::run(ld16<V8>(qrow + rowc(c)), kb[c], s);
+        dp = Mfma<T>::run(ld16<V8>(drow + rowc(c)), ld16<V8>(vlds + rowc(c)), dp);
       }
       // s[i] is S[q][kj] for query row r = 32 qh + 8 (i / 4) + 4 hi + i % 4 of the tile. Rows
       // past the sequence end have Q = dO = 0 (staged as zeros), so they add nothing to dK or
@@ -523,8 +515,16 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs 
 #pragma unroll
         for (int c2 = 0; c2 < 2; ++c2) {
           const int rb = 32 * qh + 16 * c2;
-          dva[md] = Mfma<T>::run(ld_tr<V8, RP>(dsb, rb, 32 * md, lane), pb[c2], dva[md]);
-          dka[md] = Mfma<T>::run(ld_tr<V8, RP>(qsb, rb, 32 * md, lane), sb_[c2], dka[md]);
+          V8 dot, qt_;
+          if constexpr (DMA) {
+            dot = trd.template read<V8>(dsb, rb, md);
+            qt_ = trd.template read<V8>(qsb, rb, md);
+          } else {
+            dot = ld_tr<V8, RP>(reinterpret_cast<const T*>(dsb), rb, 32 * md, lane);
+            qt_ = ld_tr<V8, RP>(reinterpret_cast<const T*>(qsb), rb, 32 * md, lane);
+          }
+          dva[md] = Mfma<T>::run(dot, pb[c2], dva[md]);
+          dka[md] = Mfma<T>::run(qt_, sb_[c2], dka[md]);
         }
     }
   }
