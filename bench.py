@@ -335,9 +335,64 @@ def stream_ceiling(dev, cfg, kernel_us, reps):
         log(f"stream ceiling {name}: probe {us:.2f} us ({blocks} blocks), kernel "
             f"{k_us if k_us is None else round(k_us, 2)} us")
     step_ms = sum(v["probe_us"] * v["launches_per_step"] for v in out.values()) * 1e-3
+    floor = launch_floor(dev, cfg, kinds, reps)
     return {"what": "esep_stream_probe (out = a (+ b)) at each kernel's bytes and launch pattern, "
                     "best of 512/1024/2048 blocks of 512 threads",
-            "kernels": out, "probe_step_ms": round(step_ms, 4)}
+            "kernels": out, "probe_step_ms": round(step_ms, 4), "floor": floor}
+
+
+def launch_floor(dev, cfg, kinds, reps):
+    """The fixed cost of the step's launch structure, measured in the same run:
+      launch_us     the time per launch of a graph of 57 nearly empty launches (esep_stream_probe
+                    over 16 bytes, one block): what each dependent launch costs before any data
+                    moves (the command processor's end-of-kernel and dispatch work);
+      launch_ms     launch_us times the step's launches (time no kernel design removes while
+                    every op is its own launch);
+      asymptote     the rate of one streaming launch over 1 GiB per stream (1 read + 1 write,
+                    2 reads + 1 write), best of 1024 / 2048 / 4096 blocks. It is below the
+                    per-launch rates at config 4's 25-75 MB sizes, whose writes the 256 MB
+                    Infinity Cache absorbs and writes back during later launches, so it bounds
+                    nothing here; it is reported for the record."""
+    import torch
+
+    from solution.body import _hip
+
+    n = 57
+    tiny = [(torch.empty(16, device=dev, dtype=torch.uint8), torch.empty(16, device=dev, dtype=torch.uint8))
+            for _ in range(n)]
+
+    def empties():
+        for a, o in tiny:
+            _hip.stream_probe(a, o, blocks=1)
+    gr = capture(empties)
+    time_graph(gr, 2)
+    ms, _ = time_graph(gr, reps)
+    launch_us = ms * 1e3 / n
+    del gr, tiny
+
+    big = 1 << 30
+    rates = {}
+    bufs = [torch.empty(big, device=dev, dtype=torch.uint8) for _ in range(3)]
+    for n_src in (1, 2):
+        best = None
+        for blocks in (1024, 2048, 4096):
+            def fn(blocks=blocks):
+                _hip.stream_probe(bufs[0], bufs[2], bufs[1] if n_src == 2 else None, blocks=blocks)
+            gr = capture(fn)
+            time_graph(gr, 1)
+            ms, _ = time_graph(gr, 5)
+            gbs = (n_src + 1) * big / (ms * 1e-3) / 1e9
+            best = gbs if best is None or gbs > best else best
+            del gr
+        rates[n_src] = best
+    del bufs
+    torch.cuda.empty_cache()
+    launches = sum(v[2] for v in kinds.values()) + 1  # + the batched weight-gradient reduce
+    log(f"launch floor: {launch_us:.2f} us per launch x {launches} launches; 1 GiB stream "
+        f"asymptotes 1R1W {rates[1]:.0f} / 2R1W {rates[2]:.0f} GB/s")
+    return {"launch_us": round(launch_us, 3), "launches_per_step": launches,
+            "launch_ms": round(launches * launch_us * 1e-3, 4),
+            "asymptote_GB/s": {"1R1W": round(rates[1], 1), "2R1W": round(rates[2], 1)}}
 
 
 def _flush_buffer(dev):

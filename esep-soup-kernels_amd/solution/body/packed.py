@@ -110,54 +110,67 @@ def _is_rmsnorm(norm):
 
 
 def _norm_eps(norm, residual, delta):
-    """The norm's eps when add_rmsnorm can stand in for norm(residual + delta), else None
-    (reference packed.py:111-140): an unmodified RMSNorm module without hooks with a 1-D
-    floating weight on the device, an fp32 residual stream on the device (a 16-bit stream keeps
-    HF's rounding), rows within NORM_BLOCK, and a floating delta shaped like the residual."""
+    """The eps add_rmsnorm runs with when it can stand in for norm(residual + delta), else None
+    after a logged fallback (the conditions of reference packed.py:111-140; this build also
+    takes a trainable weight, whose gradient the kernel's weight-gradient reduction gives)."""
     if not USE_KERNELS:
         return None
     from .norm_rope import NORM_BLOCK
 
-    if not _is_rmsnorm(norm) or _has_hooks(norm):
-        return _fallback("norm kernel", "not a plain Qwen2RMSNorm or hooks")
-    weight, eps = getattr(norm, "weight", None), getattr(norm, "variance_epsilon", None)
-    if not isinstance(weight, torch.Tensor) or eps is None:
-        return _fallback("norm kernel", "missing weight / eps")
-    if weight.dim() != 1 or weight.dtype not in _KERNEL_FLOATS or not weight.is_cuda:
-        return _fallback("norm kernel", f"weight {weight.dtype} {tuple(weight.shape)}")
-    hidden = weight.shape[0]
-    if residual.dtype != torch.float32 or not residual.is_cuda or residual.shape[-1] != hidden:
-        return _fallback("norm kernel", f"residual {residual.dtype} {residual.device}")
-    if hidden > NORM_BLOCK:
-        return _fallback("norm kernel", f"hidden {hidden} > {NORM_BLOCK}")
-    if delta is not None and (delta.dtype not in _KERNEL_FLOATS or delta.shape != residual.shape
-                              or delta.device != residual.device):
-        return _fallback("norm kernel", f"delta {delta.dtype} {tuple(delta.shape)}")
+    w = getattr(norm, "weight", None)
+    eps = getattr(norm, "variance_epsilon", None)
+    # (condition the kernel needs, why not) in order; each condition may rely on the ones before
+    needs = (
+        (lambda: _is_rmsnorm(norm) and not _has_hooks(norm),
+         lambda: "not a plain Qwen2RMSNorm or hooks"),
+        (lambda: isinstance(w, torch.Tensor) and eps is not None,
+         lambda: "no weight tensor or no variance_epsilon"),
+        (lambda: w.dim() == 1 and w.is_cuda and w.dtype in _KERNEL_FLOATS,
+         lambda: f"weight {w.dtype} {tuple(w.shape)} on {w.device}"),
+        (lambda: (residual.is_cuda and residual.dtype == torch.float32
+                  and residual.shape[-1] == w.shape[0]),
+         lambda: f"residual stream {residual.dtype} on {residual.device}"),
+        (lambda: w.shape[0] <= NORM_BLOCK,
+         lambda: f"hidden size {w.shape[0]} above {NORM_BLOCK}"),
+        (lambda: delta is None or (delta.dtype in _KERNEL_FLOATS and delta.device == residual.device
+                                   and delta.shape == residual.shape),
+         lambda: f"delta {delta.dtype} {tuple(delta.shape)}"),
+    )
+    for ok, why in needs:
+        if not ok():
+            return _fallback("norm kernel", why())
     return float(eps)
 
 
-def _add_norm(norm, residual, delta, final=False, with_eps=False, n_out=1, save_output=False):
-    """(r, norm(r)) for r = residual (+ delta); with with_eps also the eps the kernel used (None
-    when HF's norm ran). With n_out > 1 the normed output comes as a tuple of n_out tensors, one
-    per consumer (the kernel's are views whose gradients its backward sums; HF's are the same
-    tensor repeated). The kernel keeps r in fp32; the normed output of a decoder-layer norm is
-    stored in the autocast dtype (its consumers compute in it), the final norm's in HF's
-    promote(weight, residual). Reference packed.py:152-181."""
-    eps = _norm_eps(norm, residual, delta)
-    if eps is not None:
-        out_dtype = torch.promote_types(norm.weight.dtype, residual.dtype)
-        if not final and torch.is_autocast_enabled("cuda"):
-            out_dtype = torch.get_autocast_dtype("cuda")
-        if out_dtype in _KERNEL_FLOATS:
-            from .norm_rope import add_rmsnorm
+def _normed_dtype(norm, residual, final):
+    """dtype of a kernel norm's output: what its consumers compute in. A decoder-layer norm
+    feeds projections, which run in the autocast dtype under autocast; the final norm returns
+    HF's dtype, promote(weight, residual)."""
+    if not final and torch.is_autocast_enabled("cuda"):
+        return torch.get_autocast_dtype("cuda")
+    return torch.promote_types(norm.weight.dtype, residual.dtype)
 
-            r, y = add_rmsnorm(residual, delta, norm.weight, eps, out_dtype, n_out,
-                               save_output=save_output and not final)
-            return (r, y, eps) if with_eps else (r, y)
-    r = residual if delta is None else residual + delta
-    y = norm(r)
-    ys = y if n_out == 1 else (y,) * n_out
-    return (r, ys, None) if with_eps else (r, ys)
+
+def _add_norm(norm, residual, delta, final=False, with_eps=False, n_out=1, save_output=False):
+    """(r, normed) for r = residual (+ delta); with_eps appends the eps the kernel ran with
+    (None on HF's norm: the MLP recompute needs to know which ran). n_out > 1 gives one output
+    per consumer: distinct views of the kernel's single buffer (its backward adds their
+    gradients in fp32), or HF's tensor n_out times. The kernel keeps r in fp32. Reference
+    packed.py:152-181."""
+    eps = _norm_eps(norm, residual, delta)
+    out_dtype = None if eps is None else _normed_dtype(norm, residual, final)
+    if out_dtype in _KERNEL_FLOATS:
+        from .norm_rope import add_rmsnorm
+
+        r, normed = add_rmsnorm(residual, delta, norm.weight, eps, out_dtype, n_out,
+                                save_output=save_output and not final)
+    else:
+        eps = None
+        r = residual if delta is None else residual + delta
+        normed = norm(r)
+        if n_out > 1:
+            normed = tuple(normed for _ in range(n_out))
+    return (r, normed, eps) if with_eps else (r, normed)
 
 
 # ----------------------------------------------------------------------------------------
