@@ -284,6 +284,28 @@ __device__ __forceinline__ int xcd_order(int b, int C) {
 }
 inline int64_t xcd_grid(int64_t C, int64_t groups) { return (groups + 7) / 8 * 8 * C; }
 
+// xcd_order with each XCD running its groups tile-major: tile 0 of every group it holds, then
+// tile 1, and so on, in the order the hardware dispatches its workgroups. The kernels number a
+// group's tiles heaviest first (causal: the query tile with the most keys, the key tile with
+// the most queries), so every XCD starts its longest blocks before its short ones
+// (longest-processing-time first); groups stay whole on one XCD as with xcd_order. It pays when
+// the grid is resident in about one round (short inputs: the longest blocks set the kernel's
+// time); on long inputs the group-by-group order of xcd_order keeps a group's K / V (or Q / dO)
+// reads close together in time in its XCD's L2 and is faster (block_order picks).
+__device__ __forceinline__ int xcd_order_lpt(int b, int C, int groups) {
+  const int xcd = b % 8, slot = b / 8;
+  const int per_xcd = (groups + 7) / 8;
+  return (xcd + 8 * (slot % per_xcd)) * C + slot / per_xcd;
+}
+__device__ __forceinline__ int block_order(int b, int C, int groups, int lpt) {
+  return lpt ? xcd_order_lpt(b, C, groups) : xcd_order(b, C);
+}
+
+// Whether a grid of `blocks` workgroups of a kernel that keeps `per_cu` of them resident on each
+// of MI355X's 256 CUs runs longest-first (xcd_order_lpt): at most two rounds of residency.
+constexpr int64_t kAttnCUs = 256;
+inline int use_lpt(int64_t blocks, int per_cu) { return blocks <= 2 * kAttnCUs * per_cu ? 1 : 0; }
+
 // Sequence s's token range [start, end), clamped into [0, T].
 __device__ __forceinline__ void seq_bounds(const int32_t* cu, int s, int64_t T, int* start,
                                            int* end) {

@@ -244,7 +244,8 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq(const AttnBwdArgs b)
 // consumed, one barrier per tile). Same prologue as k_attn_bwd_dq; dq_tile_swz is dq_half on
 // the swizzled tiles.
 template <typename T, int NW>
-__global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq_dma(const AttnBwdArgs b, int qtiles) {
+__global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq_dma(const AttnBwdArgs b, int qtiles,
+                                                                 int lpt) {
   constexpr int D = 128;
   constexpr int BN = 32;
   using V8 = typename Mfma<T>::v8;
@@ -253,7 +254,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq_dma(const AttnBwdArg
   __shared__ __align__(1024) char kv[2][2][BN * 256];  // [buffer][K, V][swizzled tile]
 
   // XCD-aware order: the query tiles of one (sequence, head) run on one XCD
-  const int lin = xcd_order((int)blockIdx.x, qtiles);
+  const int lin = block_order((int)blockIdx.x, qtiles, a.HQ * a.n_seq, lpt);
   const int bx = lin % qtiles, rest = lin / qtiles;
   const int h = rest % a.HQ, seq = rest / a.HQ;
   if (seq >= a.n_seq) return;
@@ -329,7 +330,8 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq_dma(const AttnBwdArg
 // at config 5 the backward takes 8.4 ms with 4 and 10.8 ms with 8, at config 4 0.30 vs 0.28 ms.
 // D = 64 takes 4 wavefronts and 64-query tiles.
 template <typename T, int D, int NW, int BQ>
-__global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs b, int ktiles) {
+__global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs b, int ktiles,
+                                                               int lpt) {
   constexpr int NT = 64 * NW, BK = 32 * NW;
   using V8 = typename Mfma<T>::v8;
   const AttnArgs& a = b.f;
@@ -351,7 +353,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs 
   // XCD-aware order: the key tiles of one (sequence, kv head, part) run on one XCD (they read
   // the same Q / dO rows)
   const int split = b.split;                 // query-head groups per kv head
-  const int lin = xcd_order((int)blockIdx.x, ktiles);
+  const int lin = block_order((int)blockIdx.x, ktiles, a.HK * split * a.n_seq, lpt);
   const int bx = lin % ktiles, rest = lin / ktiles;
   const int yy = rest % (a.HK * split), seq = rest / (a.HK * split);
   if (seq >= a.n_seq) return;
@@ -585,8 +587,9 @@ hipError_t bwd_run(const AttnBwdArgs& b, int max_seqlen, hipStream_t s) {
   if constexpr (D == 128) {
     const int64_t n = xcd_grid(gq.x, (int64_t)gq.y * gq.z);
     if (n > 0x7fffffff) return hipErrorInvalidValue;
+    // 2 blocks resident per CU (launch bound)
     hipLaunchKernelGGL((k_attn_bwd_dq_dma<T, QW>), dim3((unsigned)n), dim3(64 * QW), 0, s, b,
-                       (int)gq.x);
+                       (int)gq.x, use_lpt(n, 2));
   } else {
     hipLaunchKernelGGL((k_attn_bwd_dq<T, D, QW>), gq, dim3(64 * QW), 0, s, b);
   }
@@ -601,8 +604,9 @@ hipError_t bwd_run(const AttnBwdArgs& b, int max_seqlen, hipStream_t s) {
       too_big = true;
       return;
     }
+    // resident per CU: the 8-wavefront block's LDS leaves room for one, the launch bound two
     hipLaunchKernelGGL((k_attn_bwd_dkdv<T, D, NW, BQ>), dim3((unsigned)n), dim3(64 * NW), 0, s, b,
-                       (int)ktiles);
+                       (int)ktiles, use_lpt(n, NW == 8 ? 1 : 2));
   };
   if constexpr (D == 128) {
     if (b.split > 1)

@@ -339,7 +339,8 @@ __device__ __forceinline__ void fwd_tile_swz(const char* ks, const char* vs, int
 // 32-key K / V tiles go through a ring of NBUF swizzled buffers (tile t + NBUF - 1 in flight
 // while tile t is consumed).
 template <typename T, int NBUF>
-__global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd_swz(const AttnArgs a, int qtiles) {
+__global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd_swz(const AttnArgs a, int qtiles,
+                                                                  int lpt) {
   constexpr int D = 128;
   constexpr int BN = 32;
   constexpr int TILE = BN * 256;  // bytes of one K or V tile
@@ -347,7 +348,7 @@ __global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd_swz(const AttnArgs
   __shared__ __align__(1024) char kv[NBUF][2][TILE];  // [buffer][K, V][swizzled rows]
 
   // XCD-aware order (xcd_order): the query tiles of one (sequence, head) run on one XCD.
-  const int lin = xcd_order((int)blockIdx.x, qtiles);
+  const int lin = block_order((int)blockIdx.x, qtiles, a.HQ * a.n_seq, lpt);
   const int bx = lin % qtiles, rest = lin / qtiles;
   const int h = rest % a.HQ, seq = rest / a.HQ;
   if (seq >= a.n_seq) return;
@@ -425,8 +426,9 @@ hipError_t fwd_d(const AttnArgs& a, int D, dim3 grid, hipStream_t s, bool* sup) 
   if (D == 128) {
     const int64_t n = xcd_grid(grid.x, (int64_t)grid.y * grid.z);
     if (n > 0x7fffffff) return hipErrorInvalidValue;
+    // 3 blocks resident per CU (launch bound)
     hipLaunchKernelGGL((k_attn_fwd_swz<T, 2>), dim3((unsigned)n), dim3(kAttnThreads), 0, s, a,
-                       (int)grid.x);
+                       (int)grid.x, use_lpt(n, 3));
   }
   else if (D == 64)
     hipLaunchKernelGGL((k_attn_fwd<T, 64>), grid, dim3(kAttnThreads), 0, s, a);

@@ -87,15 +87,16 @@ int64_t bwd_partials(int64_t rows, int64_t n) {
 }
 
 // Blocks per (kv head, key tile) of the attention dK / dV kernel: split the kv head's query
-// heads over more blocks (the smallest divisor of HQ / HK that gives >= 192 blocks for T tokens,
-// three quarters of the CUs), each writing fp32 partials, when one block per kv head would leave
+// heads over more blocks (the smallest divisor of HQ / HK that gives >= 384 blocks for T tokens,
+// one and a half per CU), each writing fp32 partials, when one block per kv head would leave
 // CUs idle. The partials cost traffic (at config 4, 64 key blocks of 6 query heads: split 6
-// writes and re-reads 100 MB): split 6 0.271 ms, 3 0.252 ms, 2 0.301 ms for the backward.
+// writes and re-reads 100 MB), but with the longest-first block order (xcd_order_lpt) the
+// finer split balances better: config 4 backward 0.197 ms with split 3, 0.180 ms with 6.
 int attn_split(int64_t T, int HQ, int HK) {
   const int G = HQ / HK;
   const int64_t blocks = ((T + 255) / 256) * HK;  // 256-key blocks (the D = 128 kernel)
   int s = 1;
-  while (blocks * s < 192 && s < G) {
+  while (blocks * s < 384 && s < G) {
     ++s;
     while (G % s) ++s;
   }

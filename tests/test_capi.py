@@ -194,10 +194,14 @@ def test_attention_workspace_size():
     # 1 sequence of 65536 tokens, 28/4 heads: 256-key blocks already fill the GPU, no split
     assert ws(65536, 28, 4, 128) == 28 * 65536
     # 8192 tokens, 12/2 heads: 32 x 2 blocks; the smallest divisor s of the 6 query heads of a
-    # kv head with 64 s >= 192 blocks is 3
-    assert ws(8192, 12, 2, 128) == 12 * 8192 + 2 * 3 * 8192 * 2 * 128
-    # 4096 tokens: 16 x 2 blocks, s = 6 (32 x 6 = 192)
+    # kv head with 64 s >= 384 blocks is 6
+    assert ws(8192, 12, 2, 128) == 12 * 8192 + 2 * 6 * 8192 * 2 * 128
+    # 4096 tokens: 16 x 2 blocks, s = 6 (all 6 query heads apart: 32 x 6 = 192 blocks)
     assert ws(4096, 12, 2, 128) == 12 * 4096 + 2 * 6 * 4096 * 2 * 128
+    # 32768 tokens, 28/4 heads: 128 x 4 = 512 blocks already, no split
+    assert ws(32768, 28, 4, 128) == 28 * 32768
+    # 16384 tokens, 28/4 heads: 64 x 4 = 256 blocks; s = 7 (the only divisor of 7 above 1)
+    assert ws(16384, 28, 4, 128) == 28 * 16384 + 2 * 7 * 16384 * 4 * 128
     assert ws(3, 1, 1, 64) == 4  # delta rounded up to a multiple of 4 floats
 
 
