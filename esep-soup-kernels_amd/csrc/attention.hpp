@@ -297,10 +297,6 @@ __device__ __forceinline__ int xcd_order_lpt(int b, int C, int groups) {
   const int per_xcd = (groups + 7) / 8;
   return (xcd + 8 * (slot % per_xcd)) * C + slot / per_xcd;
 }
-__device__ __forceinline__ int block_order(int b, int C, int groups, int lpt) {
-  return lpt ? xcd_order_lpt(b, C, groups) : xcd_order(b, C);
-}
-
 // Whether a grid of `blocks` workgroups of a kernel that keeps `per_cu` of them resident on each
 // of MI355X's 256 CUs runs longest-first (xcd_order_lpt): at most two rounds of residency.
 constexpr int64_t kAttnCUs = 256;
@@ -313,6 +309,58 @@ __device__ __forceinline__ void seq_bounds(const int32_t* cu, int s, int64_t T, 
   const int c0 = cu[s], c1 = cu[s + 1];
   *start = c0 < 0 ? 0 : (c0 > tt ? tt : c0);
   *end = c1 < *start ? *start : (c1 > tt ? tt : c1);
+}
+
+// The sequence of rank r when the n_seq <= 64 sequences are ordered longest first (ties by
+// index): lane s ranks sequence s against all others, and the lane holding rank r is found by
+// ballot. Every lane of the wavefront gets the answer (n_seq when r is out of range).
+__device__ __forceinline__ int seq_of_rank(const int32_t* cu, int n_seq, int64_t T, int r) {
+  const int lane = (int)(threadIdx.x & 63);
+  int len = -1;
+  if (lane < n_seq) {
+    int s, e;
+    seq_bounds(cu, lane, T, &s, &e);
+    len = e - s;
+  }
+  int rank = 0;
+  for (int j = 0; j < n_seq; ++j) {
+    const int lj = __builtin_amdgcn_readlane(len, j);
+    rank += (lj > len || (lj == len && j < lane)) ? 1 : 0;
+  }
+  const uint64_t hit = __ballot(lane < n_seq && rank == r);
+  return hit != 0 ? (int)__builtin_ctzll(hit) : n_seq;
+}
+
+// Block orders of the D = 128 attention kernels, chosen per launch (attn_order):
+//   kOrderGroups  xcd_order: each XCD runs its groups one after another;
+//   kOrderLpt     xcd_order_lpt: each XCD runs its groups tile-major, longest tiles first (grids
+//                 resident in at most two rounds);
+//   kOrderSorted  the groups (gps per sequence, sequence-major) sorted by their sequence's
+//                 length, longest first, and dealt to the 8 XCDs in snake order (XCD 0..7, then
+//                 7..0, ...): every XCD gets a near-equal share of the work and runs its groups
+//                 heaviest first, each group whole with its tiles in a row as with xcd_order
+//                 (n_seq <= 64). Dealing groups round-robin in index order instead put a
+//                 sequence's 4 kv-head groups of config 5's dK / dV on XCDs 0-3 or 4-7 by the
+//                 sequence's parity, and the two halves' work differed by 38%.
+// The result is the block's index in the group-major order (group * C + tile); a padding block
+// gets an index past the last group and exits.
+constexpr int kOrderGroups = 0, kOrderLpt = 1, kOrderSorted = 2;
+__device__ __forceinline__ int block_order(int b, int C, int groups, int mode, int gps,
+                                           const int32_t* cu, int n_seq, int64_t T) {
+  if (mode == kOrderGroups) return xcd_order(b, C);
+  if (mode == kOrderLpt) return xcd_order_lpt(b, C, groups);
+  const int xcd = b % 8, slot = b / 8;
+  const int j = slot / C, tile = slot % C;
+  const int p = 8 * j + ((j & 1) ? 7 - xcd : xcd);  // position in the sorted group list
+  if (p >= groups) return groups * C;
+  const int seq = seq_of_rank(cu, n_seq, T, p / gps);
+  return (seq * gps + p % gps) * C + tile;
+}
+
+// The order a grid of `blocks` workgroups takes when `per_cu` of them stay resident per CU.
+inline int attn_order(int64_t blocks, int per_cu, int n_seq) {
+  if (use_lpt(blocks, per_cu)) return kOrderLpt;
+  return n_seq <= 64 ? kOrderSorted : kOrderGroups;
 }
 
 // A [ROWS x D] tile (token rows r0 .. r0 + ROWS - 1 below rend; the rest reads as 0) moved

@@ -245,7 +245,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq(const AttnBwdArgs b)
 // the swizzled tiles.
 template <typename T, int NW>
 __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq_dma(const AttnBwdArgs b, int qtiles,
-                                                                 int lpt) {
+                                                                 int order) {
   constexpr int D = 128;
   constexpr int BN = 32;
   using V8 = typename Mfma<T>::v8;
@@ -254,7 +254,8 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq_dma(const AttnBwdArg
   __shared__ __align__(1024) char kv[2][2][BN * 256];  // [buffer][K, V][swizzled tile]
 
   // XCD-aware order: the query tiles of one (sequence, head) run on one XCD
-  const int lin = block_order((int)blockIdx.x, qtiles, a.HQ * a.n_seq, lpt);
+  const int lin = block_order((int)blockIdx.x, qtiles, a.HQ * a.n_seq, order, a.HQ, a.cu, a.n_seq,
+                              a.T);
   const int bx = lin % qtiles, rest = lin / qtiles;
   const int h = rest % a.HQ, seq = rest / a.HQ;
   if (seq >= a.n_seq) return;
@@ -331,7 +332,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq_dma(const AttnBwdArg
 // D = 64 takes 4 wavefronts and 64-query tiles.
 template <typename T, int D, int NW, int BQ>
 __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs b, int ktiles,
-                                                               int lpt) {
+                                                               int order) {
   constexpr int NT = 64 * NW, BK = 32 * NW;
   using V8 = typename Mfma<T>::v8;
   const AttnArgs& a = b.f;
@@ -353,7 +354,8 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs 
   // XCD-aware order: the key tiles of one (sequence, kv head, part) run on one XCD (they read
   // the same Q / dO rows)
   const int split = b.split;                 // query-head groups per kv head
-  const int lin = block_order((int)blockIdx.x, ktiles, a.HK * split * a.n_seq, lpt);
+  const int lin = block_order((int)blockIdx.x, ktiles, a.HK * split * a.n_seq, order, a.HK * split,
+                              a.cu, a.n_seq, a.T);
   const int bx = lin % ktiles, rest = lin / ktiles;
   const int yy = rest % (a.HK * split), seq = rest / (a.HK * split);
   if (seq >= a.n_seq) return;
@@ -589,7 +591,7 @@ hipError_t bwd_run(const AttnBwdArgs& b, int max_seqlen, hipStream_t s) {
     if (n > 0x7fffffff) return hipErrorInvalidValue;
     // 2 blocks resident per CU (launch bound)
     hipLaunchKernelGGL((k_attn_bwd_dq_dma<T, QW>), dim3((unsigned)n), dim3(64 * QW), 0, s, b,
-                       (int)gq.x, use_lpt(n, 2));
+                       (int)gq.x, attn_order(n, 2, b.f.n_seq));
   } else {
     hipLaunchKernelGGL((k_attn_bwd_dq<T, D, QW>), gq, dim3(64 * QW), 0, s, b);
   }
@@ -606,7 +608,7 @@ hipError_t bwd_run(const AttnBwdArgs& b, int max_seqlen, hipStream_t s) {
     }
     // resident per CU: the 8-wavefront block's LDS leaves room for one, the launch bound two
     hipLaunchKernelGGL((k_attn_bwd_dkdv<T, D, NW, BQ>), dim3((unsigned)n), dim3(64 * NW), 0, s, b,
-                       (int)ktiles, use_lpt(n, NW == 8 ? 1 : 2));
+                       (int)ktiles, attn_order(n, NW == 8 ? 1 : 2, b.f.n_seq));
   };
   if constexpr (D == 128) {
     if (b.split > 1)

@@ -340,7 +340,7 @@ __device__ __forceinline__ void fwd_tile_swz(const char* ks, const char* vs, int
 // while tile t is consumed).
 template <typename T, int NBUF>
 __global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd_swz(const AttnArgs a, int qtiles,
-                                                                  int lpt) {
+                                                                  int order) {
   constexpr int D = 128;
   constexpr int BN = 32;
   constexpr int TILE = BN * 256;  // bytes of one K or V tile
@@ -348,7 +348,8 @@ __global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd_swz(const AttnArgs
   __shared__ __align__(1024) char kv[NBUF][2][TILE];  // [buffer][K, V][swizzled rows]
 
   // XCD-aware order (xcd_order): the query tiles of one (sequence, head) run on one XCD.
-  const int lin = block_order((int)blockIdx.x, qtiles, a.HQ * a.n_seq, lpt);
+  const int lin = block_order((int)blockIdx.x, qtiles, a.HQ * a.n_seq, order, a.HQ, a.cu, a.n_seq,
+                              a.T);
   const int bx = lin % qtiles, rest = lin / qtiles;
   const int h = rest % a.HQ, seq = rest / a.HQ;
   if (seq >= a.n_seq) return;
@@ -428,7 +429,7 @@ hipError_t fwd_d(const AttnArgs& a, int D, dim3 grid, hipStream_t s, bool* sup) 
     if (n > 0x7fffffff) return hipErrorInvalidValue;
     // 3 blocks resident per CU (launch bound)
     hipLaunchKernelGGL((k_attn_fwd_swz<T, 2>), dim3((unsigned)n), dim3(kAttnThreads), 0, s, a,
-                       (int)grid.x, use_lpt(n, 3));
+                       (int)grid.x, attn_order(n, 3, a.n_seq));
   }
   else if (D == 64)
     hipLaunchKernelGGL((k_attn_fwd<T, 64>), grid, dim3(kAttnThreads), 0, s, a);

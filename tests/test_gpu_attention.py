@@ -146,15 +146,21 @@ def test_attn_bwd_deterministic():
     assert all(torch.equal(a, b) for a, b in zip(*runs))
 
 
-@pytest.mark.parametrize("lengths", [[4096] * 4, [4000, 4097, 3999, 4100]], ids=["even", "ragged"])
+@pytest.mark.parametrize("lengths", [[4096] * 4, [4000, 4097, 3999, 4100],
+                                     [3000, 4100, 2500, 4096, 3900, 1800, 4000, 3500, 2900]],
+                         ids=["even", "ragged", "ragged9"])
 def test_attn_bwd_long_sequences_sampled_keys(lengths):
-    """A config-5-like shape (4 sequences of ~4096, 28 / 4 heads, D = 128: enough key blocks that
-    the kernel does not split the query heads, so the 4-wavefront dK / dV kernel runs) checked on
-    sampled keys against float64 sums restated from the formulas (dV_j = sum_q P_qj dO_q,
-    dK_j = scale sum_q P_qj (dP_qj - delta_q) Q_q over the causal queries of every query head of
-    the kv head), with the kernel's own lse and O for P and delta. The ragged lengths put the
-    end of every sequence inside a query tile (rows past the end staged and masked); the sample
-    takes keys from the last 40 tokens of each sequence as well as from anywhere."""
+    """A config-5-like shape (4 or 9 sequences of up to ~4096, 28 / 4 heads, D = 128: enough key
+    blocks that the kernel does not split the query heads, so the 4-wavefront dK / dV kernel
+    runs) checked on sampled keys against float64 sums restated from the formulas
+    (dV_j = sum_q P_qj dO_q, dK_j = scale sum_q P_qj (dP_qj - delta_q) Q_q over the causal
+    queries of every query head of the kv head), with the kernel's own lse and O for P and delta,
+    and on sampled queries (O_q = sum_j P_qj V_j / l_q, dQ_q = scale sum_j P_qj (dP_qj - delta_q)
+    K_j over the causal keys). The ragged lengths put the end of every sequence inside a query
+    tile (rows past the end staged and masked); the sample takes keys from the last 40 tokens of
+    each sequence as well as from anywhere. These grids are too large for the longest-first
+    block order, so the forward and dQ kernels (and, with 9 sequences, the dK / dV kernel) run
+    the length-sorted XCD order (kOrderSorted), equal-length sequences ranked by index."""
     from solution.body import _hip
 
     HQ, HK, D = 28, 4, 128
@@ -191,3 +197,21 @@ def test_attn_bwd_long_sequences_sampled_keys(lengths):
                 err = np.abs(got - want)
                 assert np.all(err <= 1e-2 * np.abs(want).max() + 1e-2 * np.abs(want) + 1e-5), \
                     (name, j, hk, err.max(), np.abs(want).max())
+    DQ = np64(dq)
+    for i in sorted(set(rng.choice(T, 12, replace=False).tolist() + tails)):
+        s_start = bounds[np.searchsorted(bounds, i, side="right") - 1]
+        kk = np.arange(s_start, i + 1)  # causal keys of query i
+        for h in range(HQ):
+            hk = h // G
+            s_ = scale * (K[kk, hk] @ Q[i, h])
+            p = np.exp(s_ - s_.max())
+            p /= p.sum()
+            want_o = p @ V[kk, hk]
+            pk = np.exp(scale * (K[kk, hk] @ Q[i, h]) - L[h, i])
+            dp = V[kk, hk] @ DO[i, h]
+            delta = np.sum(DO[i, h] * O[i, h])
+            want_dq = scale * ((pk * (dp - delta)) @ K[kk, hk])
+            for name, got, want in (("o", O[i, h], want_o), ("dq", DQ[i, h], want_dq)):
+                err = np.abs(got - want)
+                assert np.all(err <= 1e-2 * np.abs(want).max() + 1e-2 * np.abs(want) + 1e-5), \
+                    (name, i, h, err.max(), np.abs(want).max())
