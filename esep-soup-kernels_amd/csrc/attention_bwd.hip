@@ -10,7 +10,7 @@
 // dQ^T += K^T dS^T with K^T read transposed (ds_read_b64_tr_b16) out of the row-major K tile and
 // dS^T fed from registers in the permuted key order (the forward's P V trick).
 //
-// k_attn_bwd_dkdv: one block per (256 keys at D = 128, 128 at D = 64; kv head; part of the kv
+// k_attn_bwd_dkdv: one block per (128 keys; kv head; part of the kv
 // head's query heads); wavefront w owns keys 32w..32w+31 and holds their K in registers as B
 // operands (V's come from the block's V rows in LDS). It
 // walks, for each of its query heads in turn and each query tile at or after its keys (at
@@ -324,12 +324,11 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq_dma(const AttnBwdArg
                      a.scale);
 }
 
-// dK / dV blocks: NW wavefronts (32 keys each) and query tiles of BQ rows. D = 128 takes two
-// shapes: 8 wavefronts (256 keys, one block per CU by LDS) when the query heads of a kv head
-// are split over blocks (short inputs: the split parts supply the parallelism), and 4 wavefronts
-// with 32-query tiles (two blocks per CU, each hiding the other's barriers) when they are not:
-// at config 5 the backward takes 8.4 ms with 4 and 10.8 ms with 8, at config 4 0.30 vs 0.28 ms.
-// D = 64 takes 4 wavefronts and 64-query tiles.
+// dK / dV blocks: NW wavefronts (32 keys each) and query tiles of BQ rows. D = 128 takes 4
+// wavefronts with 32-query tiles (two blocks per CU, each hiding the other's barriers); 8
+// wavefronts (256 keys, one block per CU by LDS) measured slower at config 5 (backward 10.8
+// against 8.4 ms when tuned) and, with the longest-first block order, at config 4 (0.182 against
+// 0.171 ms with the query heads split six ways). D = 64 takes 4 wavefronts and 64-query tiles.
 template <typename T, int D, int NW, int BQ>
 __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs b, int ktiles,
                                                                int order) {
@@ -606,15 +605,12 @@ hipError_t bwd_run(const AttnBwdArgs& b, int max_seqlen, hipStream_t s) {
       too_big = true;
       return;
     }
-    // resident per CU: the 8-wavefront block's LDS leaves room for one, the launch bound two
+    // 2 blocks resident per CU (launch bound)
     hipLaunchKernelGGL((k_attn_bwd_dkdv<T, D, NW, BQ>), dim3((unsigned)n), dim3(64 * NW), 0, s, b,
-                       (int)ktiles, attn_order(n, NW == 8 ? 1 : 2, b.f.n_seq));
+                       (int)ktiles, attn_order(n, 2, b.f.n_seq));
   };
   if constexpr (D == 128) {
-    if (b.split > 1)
-      dkdv(std::integral_constant<int, 8>{}, std::integral_constant<int, 64>{});
-    else
-      dkdv(std::integral_constant<int, 4>{}, std::integral_constant<int, 32>{});
+    dkdv(std::integral_constant<int, 4>{}, std::integral_constant<int, 32>{});
   } else {
     dkdv(std::integral_constant<int, 4>{}, std::integral_constant<int, 64>{});
   }

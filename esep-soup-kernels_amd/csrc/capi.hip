@@ -87,14 +87,16 @@ int64_t bwd_partials(int64_t rows, int64_t n) {
 }
 
 // Blocks per (kv head, key tile) of the attention dK / dV kernel: split the kv head's query
-// heads over more blocks (the smallest divisor of HQ / HK that gives >= 384 blocks for T tokens,
-// one and a half per CU), each writing fp32 partials, when one block per kv head would leave
-// CUs idle. The partials cost traffic (at config 4, 64 key blocks of 6 query heads: split 6
-// writes and re-reads 100 MB), but with the longest-first block order (xcd_order_lpt) the
-// finer split balances better: config 4 backward 0.197 ms with split 3, 0.180 ms with 6.
+// heads over more blocks, each writing fp32 partials, when one block per (kv head, 128-key tile)
+// would leave the GPU short of work. The rule counts 256-token key spans per kv head and takes
+// the smallest divisor s of HQ / HK with spans * s >= 384 (768 of the kernel's 128-key blocks,
+// one and a half rounds of its two blocks per CU); it depends on the shape only. The partials
+// cost traffic (at config 4 a 6-way split writes and re-reads 100 MB), but with the
+// longest-first block order (xcd_order_lpt) the finer split balances better: config 4 backward
+// 0.182 ms with split 3, 0.171 ms with 6.
 int attn_split(int64_t T, int HQ, int HK) {
   const int G = HQ / HK;
-  const int64_t blocks = ((T + 255) / 256) * HK;  // 256-key blocks (the D = 128 kernel)
+  const int64_t blocks = ((T + 255) / 256) * HK;  // 256-token key spans
   int s = 1;
   while (blocks * s < 384 && s < G) {
     ++s;
