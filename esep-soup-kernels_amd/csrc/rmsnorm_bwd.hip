@@ -21,8 +21,19 @@ static hipError_t bwd_nv(const BwdArgs& a, int nv, dim3 grid, dim3 block, size_t
   const bool fast = a.fast != 0;
   if (a.fast == 1) {
     if (block.x > (unsigned)kBwdPipeThreads || a.wpr != 1) return hipErrorInvalidValue;
-    if (nv == 2) hipLaunchKernelGGL((k_rmsnorm_bwd_pipe<2, TX, TDY, TO>), grid, block, lds, s, a);
-    else hipLaunchKernelGGL((k_rmsnorm_bwd_pipe<3, TX, TDY, TO>), grid, block, lds, s, a);
+    // saved rstd and dx only (the common call) run a form with those parts fixed
+    const bool common = a.rstd != nullptr && a.dr == nullptr && a.dx != nullptr;
+    const int fix = common ? (a.part != nullptr ? 1 : 2) : 0;
+    if (fix == 1) {
+      if (nv == 2) hipLaunchKernelGGL((k_rmsnorm_bwd_pipe<2, TX, TDY, TO, 1>), grid, block, lds, s, a);
+      else hipLaunchKernelGGL((k_rmsnorm_bwd_pipe<3, TX, TDY, TO, 1>), grid, block, lds, s, a);
+    } else if (fix == 2) {
+      if (nv == 2) hipLaunchKernelGGL((k_rmsnorm_bwd_pipe<2, TX, TDY, TO, 2>), grid, block, lds, s, a);
+      else hipLaunchKernelGGL((k_rmsnorm_bwd_pipe<3, TX, TDY, TO, 2>), grid, block, lds, s, a);
+    } else {
+      if (nv == 2) hipLaunchKernelGGL((k_rmsnorm_bwd_pipe<2, TX, TDY, TO, 0>), grid, block, lds, s, a);
+      else hipLaunchKernelGGL((k_rmsnorm_bwd_pipe<3, TX, TDY, TO, 0>), grid, block, lds, s, a);
+    }
     return hipGetLastError();
   }
   if (a.fast == 2) {
