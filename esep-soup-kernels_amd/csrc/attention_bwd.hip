@@ -109,6 +109,7 @@ __device__ __forceinline__ void dq_tile_swz(const char* ks, const char* vs, int 
                                             f32x16 (&dqa)[4]) {
   using V8 = typename Mfma<T>::v8;
   const int hi = lane >> 5;
+  __builtin_amdgcn_s_setprio(1);  // MFMA runs at raised priority, as in the forward
   f32x16 s = f32x16{}, dp = f32x16{};
   const uint32_t r0 = swz_row_base(lane);
   constexpr int KA = 3;
@@ -142,6 +143,7 @@ __device__ __forceinline__ void dq_tile_swz(const char* ks, const char* vs, int 
       if (kj > qi) s[i] = -INFINITY;
     }
   }
+  __builtin_amdgcn_s_setprio(0);
   V8 dsb[2];
 #pragma unroll
   for (int i = 0; i < 16; ++i) {
@@ -149,12 +151,14 @@ __device__ __forceinline__ void dq_tile_swz(const char* ks, const char* vs, int 
     dsb[i / 8][i % 8] = (T)(p * (dp[i] - delta));
   }
   __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     dqa[j / 2] = Mfma<T>::run(tbuf[j % TA], dsb[j % 2], dqa[j / 2]);
     if (j + TA < 8) tbuf[j % TA] = kt.template read<V8>(ks, 16 * ((j + TA) & 1), (j + TA) >> 1);
     __builtin_amdgcn_sched_barrier(0);
   }
+  __builtin_amdgcn_s_setprio(0);
 }
 
 // 2 wavefronts per SIMD without spills (unbounded, the compiler settles at 1).
@@ -479,6 +483,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs 
     // one 32-query half at a time
 #pragma unroll
     for (int qh = 0; qh < BQ / 32; ++qh) {
+      __builtin_amdgcn_s_setprio(1);  // MFMA runs at raised priority, as in the forward
       f32x16 s = f32x16{}, dp = f32x16{};
       const char* qrow = qsb + 32 * qh * ROWB;
       const char* drow = dsb + 32 * qh * ROWB;
@@ -487,6 +492,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs 
         s = Mfma<T>::run(ld16<V8>(qrow + rowc(c)), kb[c], s);
         dp = Mfma<T>::run(ld16<V8>(drow + rowc(c)), ld16<V8>(vlds + rowc(c)), dp);
       }
+      __builtin_amdgcn_s_setprio(0);
       // s[i] is S[q][kj] for query row r = 32 qh + 8 (i / 4) + 4 hi + i % 4 of the tile. Rows
       // past the sequence end have Q = dO = 0 (staged as zeros), so they add nothing to dK or
       // dV whatever their p; only the causal mask needs applying, and only on the half-tiles
@@ -512,6 +518,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs 
           sb_[i / 8][i % 8] = (T)(p * (dp[i] - dr[e]));
         }
       }
+      __builtin_amdgcn_s_setprio(1);
       // dV^T += dO^T P and dK^T += Q^T dS, queries in the permuted order of pb / sb_
 #pragma unroll
       for (int md = 0; md < D / 32; ++md)
@@ -529,6 +536,7 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs 
           dva[md] = Mfma<T>::run(dot, pb[c2], dva[md]);
           dka[md] = Mfma<T>::run(qt_, sb_[c2], dka[md]);
         }
+      __builtin_amdgcn_s_setprio(0);
     }
   }
   if (!kok) return;

@@ -273,6 +273,11 @@ __device__ __forceinline__ void fwd_tile_swz(const char* ks, const char* vs, int
                                              f32x16 (&oacc)[4], float& m, float& l) {
   using V8 = typename Mfma<T>::v8;
   const int lq = lane & 31, hi = lane >> 5;
+  // The MFMA runs go at raised wave priority, the softmax between them at the normal one: with
+  // several wavefronts per SIMD the arbiter then feeds the matrix core from a wavefront in its
+  // MFMA run ahead of another's vector work (all three kernels; config 5: forward 1.44 -> 1.43
+  // ms, backward 5.00 -> 4.91 ms).
+  __builtin_amdgcn_s_setprio(1);
   f32x16 acc = f32x16{};
   const uint32_t k0 = swz_row_base(lane);
   constexpr int KA = 3;
@@ -294,6 +299,7 @@ __device__ __forceinline__ void fwd_tile_swz(const char* ks, const char* vs, int
 #pragma unroll
   for (int j = 0; j < VA; ++j) vbuf[j] = ldv(j);
   __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_setprio(0);
   if (kh + 31 > qw0) {
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -327,12 +333,14 @@ __device__ __forceinline__ void fwd_tile_swz(const char* ks, const char* vs, int
     for (int md = 0; md < 4; ++md) oacc[md] *= alpha;
   }
   __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_setprio(1);
 #pragma unroll
   for (int j = 0; j < 8; ++j) {
     oacc[j / 2] = Mfma<T>::run(vbuf[j % VA], pb[j % 2], oacc[j / 2]);
     if (j + VA < 8) vbuf[j % VA] = ldv(j + VA);
     __builtin_amdgcn_sched_barrier(0);
   }
+  __builtin_amdgcn_s_setprio(0);
 }
 
 // The D = 128 forward kernel: blocks, queries and the online softmax as k_attn_fwd_dma; the
