@@ -221,6 +221,24 @@ struct SwzFill {
       lds_dma_x4(base + (int64_t)r * rs + 16 * lchunk, dst + 1024 * q);
     }
   }
+
+  // Consecutive whole tiles: `cur` (an SGPR pair) addresses this wavefront's first 4-row group
+  // of the next tile and moves ROWS rows per tile; the wavefront's other groups of a tile are
+  // per-lane offsets from it. A tile then costs one 64-bit add instead of a 64-bit multiply and
+  // add per DMA instruction (forward: config 5 1.46 -> 1.445 ms, the packed decoder's shape
+  // 39.3 -> 38.0 us; the backward unchanged).
+  const char* cur;
+  int64_t tstep;
+  __device__ __forceinline__ void seq_begin(const char* base, int r0) {
+    cur = base + (int64_t)(r0 + 4 * w) * rs;
+    tstep = (int64_t)ROWS * rs;
+  }
+  __device__ __forceinline__ void seq_whole(char* dst) {
+#pragma unroll
+    for (int i = 0; i < ROWS / (4 * NW); ++i)
+      lds_dma_x4_s(cur, voff + (uint32_t)(4 * NW * i) * (uint32_t)rs, dst + 1024 * (w + NW * i));
+    cur += tstep;
+  }
 };
 
 // Two tiles of the same rows (e.g. K and V) with one whole-or-partial decision.

@@ -307,9 +307,18 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq_dma(const AttnBwdArg
   const int ntiles = (kend - start + BN - 1) / BN;
   // wavefront w fills row groups w and w + NW of the K and V tiles (rows past kend repeat row
   // kend - 1: finite data, always masked)
-  const SwzFill<BN, NW> fk(lane, w, a.k_rs * (int64_t)sizeof(T));
-  const SwzFill<BN, NW> fv(lane, w, a.v_rs * (int64_t)sizeof(T));
-  auto issue = [&](char* kd, char* vd, int kt) { swz_fill2(fk, kd, kbase, fv, vd, vbase, kt, kend); };
+  SwzFill<BN, NW> fk(lane, w, a.k_rs * (int64_t)sizeof(T));
+  SwzFill<BN, NW> fv(lane, w, a.v_rs * (int64_t)sizeof(T));
+  fk.seq_begin(kbase, start);  // tiles are issued in order: whole ones step the running addresses
+  fv.seq_begin(vbase, start);
+  auto issue = [&](char* kd, char* vd, int kt) {
+    if (kt + BN <= kend) {
+      fk.seq_whole(kd);
+      fv.seq_whole(vd);
+    } else {
+      swz_fill2(fk, kd, kbase, fv, vd, vbase, kt, kend);
+    }
+  };
 
   if (ntiles > 0) issue(kv[0][0], kv[0][1], start);
   for (int t = 0; t < ntiles; ++t) {
@@ -425,13 +434,24 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs 
   const int wu = __builtin_amdgcn_readfirstlane(w);
   // DMA path: wavefront w fills row groups w, w + NW, ... of the swizzled Q and dO tiles (rows
   // past the sequence end repeat its last row) and wavefront 0 the lse / delta words
-  const SwzFill<BQ, NW> fq(lane, wu, a.q_rs * (int64_t)sizeof(T));
-  const SwzFill<BQ, NW> fd(lane, wu, b.do_rs * (int64_t)sizeof(T));
+  // items are issued in order: a query head's whole tiles step the fillers' running addresses
+  SwzFill<BQ, NW> fq(lane, wu, a.q_rs * (int64_t)sizeof(T));
+  SwzFill<BQ, NW> fd(lane, wu, b.do_rs * (int64_t)sizeof(T));
   auto issue = [&](int it, int buf) {
     const int h = h0 + it / nqt, qt = k0 + (it % nqt) * BQ;
     const int64_t col = (int64_t)h * D;
-    swz_fill2(fq, qs[buf], reinterpret_cast<const char*>(static_cast<const T*>(a.q) + col), fd,
-              ds_[buf], reinterpret_cast<const char*>(static_cast<const T*>(b.dout) + col), qt, end);
+    const char* qbase = reinterpret_cast<const char*>(static_cast<const T*>(a.q) + col);
+    const char* dbase = reinterpret_cast<const char*>(static_cast<const T*>(b.dout) + col);
+    if (it % nqt == 0) {
+      fq.seq_begin(qbase, k0);
+      fd.seq_begin(dbase, k0);
+    }
+    if (qt + BQ <= end) {
+      fq.seq_whole(qs[buf]);
+      fd.seq_whole(ds_[buf]);
+    } else {
+      swz_fill2(fq, qs[buf], qbase, fd, ds_[buf], dbase, qt, end);
+    }
     if (wu == 0) {
 #pragma unroll
       for (int k = 0; k < 2 * BQ / 64; ++k) {

@@ -394,10 +394,18 @@ __global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd_swz(const AttnArgs
   const int ntiles = (kend - start + BN - 1) / BN;
 
   // Wavefront w fills row groups w and w + 4 of the K and V tiles (rows past kend repeat row
-  // kend - 1: finite data, always masked).
-  const SwzFill<BN, 4> fk(lane, w, krs), fv(lane, w, vrs);
+  // kend - 1: finite data, always masked). Tiles are issued in order, so whole ones step the
+  // fillers' running addresses.
+  SwzFill<BN, 4> fk(lane, w, krs), fv(lane, w, vrs);
+  fk.seq_begin(kbase, start);
+  fv.seq_begin(vbase, start);
   auto issue = [&](int buf, int kt) {
-    swz_fill2(fk, kv[buf][0], kbase, fv, kv[buf][1], vbase, kt, kend);
+    if (kt + BN <= kend) {
+      fk.seq_whole(kv[buf][0]);
+      fv.seq_whole(kv[buf][1]);
+    } else {
+      swz_fill2(fk, kv[buf][0], kbase, fv, kv[buf][1], vbase, kt, kend);
+    }
   };
 
 #pragma unroll
