@@ -373,6 +373,32 @@ def test_rmsnorm_vs_oracle(dtype, n, recompute):
     assert_close(np64(dw), dw64, 1e-4 * np.abs(dw64).max(), 1e-4, "dw")
 
 
+@pytest.mark.parametrize("dtype", [torch.bfloat16, torch.float16])
+@pytest.mark.parametrize("n", [1536, 896, 1000])
+@pytest.mark.parametrize("recompute", [False, True], ids=["saved_rstd", "recomputed_rstd"])
+def test_rmsnorm_dx_independent_of_weight_grad(dtype, n, recompute):
+    """The backward runs a form of its kernel fixed to the call (saved rstd, dx only, with or
+    without the weight gradient): dx is the same bits whether or not the weight gradient is
+    taken, and within the bar of the fp64 oracle."""
+    nr = _nr()
+    g = gen(900 + n)
+    T = 300
+    x = randn((T, n), g, dtype=dtype).requires_grad_()
+    wv = 1 + 0.02 * torch.randn(n, generator=g)
+    w1 = wv.to(DEV).requires_grad_()
+    w0 = wv.to(DEV)
+    dy = randn((T, n), g, dtype=dtype)
+    y1 = nr.rmsnorm(x, w1, EPS, recompute_rstd=recompute)
+    dx1, dw1 = torch.autograd.grad(y1, [x, w1], dy)
+    y0 = nr.rmsnorm(x, w0, EPS, recompute_rstd=recompute)
+    (dx0,) = torch.autograd.grad(y0, [x], dy)
+    assert torch.equal(y0, y1)
+    assert torch.equal(dx0, dx1)
+    dx64, dw64 = ref.rmsnorm_bwd(np64(dy), np64(x), np64(wv), EPS)
+    assert_close(np64(dx0), ref.round_to(dx64, STORE[dtype]), 2e-3, 1e-2, "dx")
+    assert_close(np64(dw1), dw64, 1e-4 * np.abs(dw64).max(), 1e-4, "dw")
+
+
 def test_rmsnorm_recompute_matches_saved_bitwise():
     """The rstd-recompute backward computes rstd with the forward's own arithmetic: its dx and
     dw equal the saved-rstd backward's bit for bit."""
