@@ -488,20 +488,28 @@ def run_small_configs(dev, reps):
     }
     flush = _flush_buffer(dev)
     out = {}
+    per_graph = 10
     for name, (what, fn, nbytes, T) in cases.items():
         gr = capture(fn)
         time_graph(gr, 3)
         res_ms, _ = time_graph(gr, reps)
         fl_ms = time_flushed(gr, flush, reps)
+        # the same step captured 10 times in one graph: a graph replay's own start-up (several
+        # microseconds, a large share of these short steps) spread over 10 steps, as in a
+        # training step that captures many layers in one graph
+        gr10 = capture(lambda: [fn() for _ in range(per_graph)])
+        time_graph(gr10, 2)
+        g10_ms = time_graph(gr10, reps)[0] / per_graph
         row = {"workload": what, "bytes_per_step": nbytes, "tokens": T}
-        for tag, ms in (("cache_resident", res_ms), ("flushed", fl_ms)):
+        for tag, ms in (("cache_resident", res_ms), ("flushed", fl_ms),
+                        ("cache_resident_10_steps_per_graph", g10_ms)):
             gbs = nbytes / (ms * 1e-3) / 1e9
             row[tag] = {"us_per_step": round(ms * 1e3, 2), "GB/s": round(gbs, 1),
                         "frac_of_peak": round(gbs / PEAK_GBS, 4), "tokens_per_s": round(T / (ms * 1e-3), 1)}
-        log(f"{name}: cache-resident {res_ms * 1e3:.1f} us, flushed {fl_ms * 1e3:.1f} us per step "
-            f"({nbytes / 1e6:.1f} MB)")
+        log(f"{name}: cache-resident {res_ms * 1e3:.1f} us, flushed {fl_ms * 1e3:.1f} us, "
+            f"10 steps per graph {g10_ms * 1e3:.1f} us per step ({nbytes / 1e6:.1f} MB)")
         out[name] = row
-        del gr
+        del gr, gr10
     del flush, c1, c2, c3n, c3r
     torch.cuda.empty_cache()
     return out
