@@ -505,6 +505,11 @@ int esep_rope(const void* q, const int64_t q_strides[3], const void* q_delta,
   return 0;
 }
 
+// Token strides of the attention tensors, in elements, at most 2^22 (8 MiB of 16-bit
+// elements): the LDS-DMA tile fills address a wavefront's rows with 32-bit per-lane byte
+// offsets of up to 20 strides from an SGPR base.
+constexpr int64_t kAttnMaxStride = int64_t{1} << 22;
+
 int esep_attn_fwd(const void* q, int64_t q_rs, const void* k, int64_t k_rs, const void* v,
                   int64_t v_rs, void* o, int64_t o_rs, float* lse, int dt, int64_t T, int HQ,
                   int HK, int D, const int32_t* cu_seqlens, int n_seq, int max_seqlen,
@@ -519,6 +524,9 @@ int esep_attn_fwd(const void* q, int64_t q_rs, const void* k, int64_t k_rs, cons
   if (q_rs < (int64_t)HQ * D || o_rs < (int64_t)HQ * D || k_rs < (int64_t)HK * D ||
       v_rs < (int64_t)HK * D)
     return fail(ESEP_ESHAPE, "attn_fwd: token stride smaller than heads * D");
+  if (q_rs > kAttnMaxStride || o_rs > kAttnMaxStride || k_rs > kAttnMaxStride ||
+      v_rs > kAttnMaxStride)
+    return fail(ESEP_ESHAPE, "attn_fwd: token stride above %lld elements", (long long)kAttnMaxStride);
   if (T == 0 || n_seq == 0 || max_seqlen == 0) return 0;
   if (q == nullptr || k == nullptr || v == nullptr || o == nullptr || cu_seqlens == nullptr)
     return fail(ESEP_EINVAL, "attn_fwd: q, k, v, o and cu_seqlens are required");
@@ -574,6 +582,10 @@ int esep_attn_bwd(const void* q, int64_t q_rs, const void* k, int64_t k_rs, cons
   if (q_rs < wq || o_rs < wq || do_rs < wq || dq_rs < wq || k_rs < wk || v_rs < wk ||
       dk_rs < wk || dv_rs < wk)
     return fail(ESEP_ESHAPE, "attn_bwd: token stride smaller than heads * D");
+  for (int64_t rs : {q_rs, o_rs, do_rs, dq_rs, k_rs, v_rs, dk_rs, dv_rs})
+    if (rs > kAttnMaxStride)
+      return fail(ESEP_ESHAPE, "attn_bwd: token stride above %lld elements",
+                  (long long)kAttnMaxStride);
   if (T == 0 || n_seq == 0 || max_seqlen == 0) return 0;
   const void* ptrs[] = {q, k, v, o, dout, dq, dk, dv};
   for (const void* p : ptrs)

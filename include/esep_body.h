@@ -233,6 +233,7 @@ int esep_rope(const void* q, const int64_t q_strides[3],
  *
  *   q [T, HQ, D], k, v [T, HK, D], o [T, HQ, D]    dt (fp16 or bf16), heads of a token
  *                                                  contiguous, token strides q_rs ... o_rs
+ *                                                  (multiples of 8, at most 2^22 elements)
  *   cu_seqlens int32 [n_seq + 1]                   sequence s is tokens [cu[s], cu[s+1]);
  *                                                  offsets are clamped into [0, T]
  *   max_seqlen >= every sequence length            (sizes the launch)

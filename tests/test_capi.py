@@ -163,6 +163,8 @@ def test_attention_validation():
     assert fwd(D=96) == -2
     assert fwd(HQ=3, HK=2) == -2  # query heads must be a multiple of kv heads
     assert fwd(q_rs=128) == -2  # token stride below HQ * D
+    assert fwd(k_rs=(1 << 22) + 8) == -2 and b"above" in lib.esep_last_error()
+    assert fwd(k_rs=1 << 22, v_rs=1 << 22, T=0) == 0  # the cap itself is accepted
     assert fwd(q=None) == -1
     assert fwd(cu=None) == -1
     assert fwd(q=8) == -3 and b"alignment" in lib.esep_last_error()
@@ -183,6 +185,7 @@ def test_attention_validation():
     assert bwd(dk=None) == -1
     assert bwd(ws=8) == -3
     assert bwd(dv_rs=100) == -2
+    assert bwd(do_rs=(1 << 22) + 8) == -2
     assert bwd(T=0) == 0
 
 
