@@ -399,6 +399,32 @@ def test_rmsnorm_dx_independent_of_weight_grad(dtype, n, recompute):
     assert_close(np64(dw1), dw64, 1e-4 * np.abs(dw64).max(), 1e-4, "dw")
 
 
+@pytest.mark.parametrize("n", [64, 1536])
+def test_rmsnorm_bwd_many_rows_per_wavefront(n):
+    """Past 64 rows per wavefront the pipelined backward reloads its window of saved rstd values
+    (one vector load per 64 rows): 150000 rows of 64 columns give ~147 rows per wavefront with
+    the weight gradient (256 blocks) and ~73 without it (512 blocks); 40000 rows of 1536 give
+    ~39 and ~20. dx on rows from every window and dw against the fp64 oracle, and dx the same
+    bits with and without the weight gradient."""
+    nr = _nr()
+    g = gen(77 + n)
+    T = 150000 if n == 64 else 40000
+    x = randn((T, n), g, dtype=torch.bfloat16).requires_grad_()
+    wv = 1 + 0.02 * torch.randn(n, generator=g)
+    w1 = wv.to(DEV).requires_grad_()
+    dy = randn((T, n), g, dtype=torch.bfloat16)
+    y = nr.rmsnorm(x, w1, EPS)
+    dx1, dw1 = torch.autograd.grad(y, [x, w1], dy)
+    y0 = nr.rmsnorm(x, wv.to(DEV), EPS)
+    (dx0,) = torch.autograd.grad(y0, [x], dy)
+    assert torch.equal(dx0, dx1)
+    rows = sorted(set([0, 1, T - 1] + torch.randint(0, T, (509,), generator=gen(5)).tolist()))
+    dx64, _ = ref.rmsnorm_bwd(np64(dy[rows]), np64(x[rows]), np64(wv), EPS)
+    assert_close(np64(dx1[rows]), ref.round_to(dx64, "bf16"), 2e-3, 1e-2, "dx")
+    _, dw64 = ref.rmsnorm_bwd(np64(dy), np64(x), np64(wv), EPS)
+    assert_close(np64(dw1), dw64, 1e-5 * np.abs(dw64).max(), 1e-5, "dw")
+
+
 def test_rmsnorm_recompute_matches_saved_bitwise():
     """The rstd-recompute backward computes rstd with the forward's own arithmetic: its dx and
     dw equal the saved-rstd backward's bit for bit."""
