@@ -200,8 +200,11 @@ struct SwzFill {
   static_assert(NW % 4 == 0 && ROWS % (4 * NW) == 0, "groups per wavefront");
   int w, lrow, lchunk;
   int64_t rs;
+  const char* cur;  // seq_begin / seq_whole: the next whole tile's first row group
+  int64_t tstep;    // bytes of ROWS token rows
   uint32_t voff;
-  __device__ __forceinline__ SwzFill(int lane, int w_, int64_t rs_) : w(w_), rs(rs_) {
+  __device__ __forceinline__ SwzFill(int lane, int w_, int64_t rs_)
+      : w(w_), rs(rs_), cur(nullptr), tstep(0) {
     lrow = lane >> 4;
     lchunk = (lane & 15) ^ (4 * lrow + (w & 3));  // swz(4 q + lrow) with q & 3 = w & 3
     voff = (uint32_t)(lrow * rs) + 16u * (uint32_t)lchunk;
@@ -227,8 +230,6 @@ struct SwzFill {
   // per-lane offsets from it. A tile then costs one 64-bit add instead of a 64-bit multiply and
   // add per DMA instruction (forward: config 5 1.46 -> 1.445 ms, the packed decoder's shape
   // 39.3 -> 38.0 us; the backward unchanged).
-  const char* cur;
-  int64_t tstep;
   __device__ __forceinline__ void seq_begin(const char* base, int r0) {
     cur = base + (int64_t)(r0 + 4 * w) * rs;
     tstep = (int64_t)ROWS * rs;
