@@ -99,3 +99,35 @@ def test_rows_ld_rejects_strided_and_expanded_rows():
                 torch.zeros(n).expand(4, n), torch.zeros(1, 1).expand(3, n)):
         with pytest.raises(_hip.EsepError):
             _hip._rows_ld(bad, n)
+
+
+def test_warmup_in_a_fresh_interpreter():
+    """Reference test_warmup.py:21-54 runs the warmup in a fresh interpreter. Here the kernels are
+    compiled ahead of time, so warmup() only loads the library: after it, the binding holds the
+    loaded handle (no load at the first step). With the library missing it does not raise (best
+    effort, as the reference's), and the first real use raises EsepError naming the build step."""
+    import os
+
+    root = Path(__file__).resolve().parent.parent
+    env = dict(os.environ, PYTHONPATH=f"{root / 'esep-soup-kernels_amd'}{os.pathsep}{root}")
+    ok = ("from solution.body import warmup, _hip\n"
+          "assert _hip._lib is None\n"
+          "warmup()\n"
+          "assert _hip._lib is not None and _hip.lib() is _hip._lib\n"
+          "print('loaded')\n")
+    r = subprocess.run([sys.executable, "-c", ok], env=env, capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 0 and "loaded" in r.stdout, r.stderr[-2000:]
+    missing = ("from pathlib import Path\n"
+               "from solution.body import warmup, _hip\n"
+               "_hip.LIB_PATH = Path('/nonexistent/libesep_body.so')\n"
+               "warmup()\n"
+               "assert _hip._lib is None\n"
+               "try:\n"
+               "    _hip.lib()\n"
+               "except _hip.EsepError as e:\n"
+               "    assert 'build' in str(e)\n"
+               "    print('raised')\n")
+    r = subprocess.run([sys.executable, "-c", missing], env=env, capture_output=True, text=True,
+                       timeout=300)
+    assert r.returncode == 0 and "raised" in r.stdout, r.stderr[-2000:]
