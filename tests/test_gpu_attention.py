@@ -251,3 +251,32 @@ def test_attn_many_sequences_block_orders(n_seq):
         err = np.abs(g64 - w64)
         assert np.all(err <= 1e-2 * np.abs(w64).max() + 1e-2 * np.abs(w64) + 1e-5), \
             (name, float(err.max()), float(np.abs(w64).max()))
+
+
+def test_attn_config4_shape():
+    """Config 4's attention as bench.py times it: 8 rows of 1024 tokens, 12 / 2 heads, D = 128,
+    bf16 (a grid of one residency round: the longest-first block order; the dK / dV kernel with
+    the query heads of a kv head split six ways and the partials' reduce). Output and gradients
+    against torch's SDPA in float32 from the same bf16 inputs, within 1e-2 of the largest
+    magnitude plus 1e-2 relative."""
+    from solution.body import _hip
+
+    lengths = [1024] * 8
+    HQ, HK, D = 12, 2, 128
+    q, k, v, cu = _inputs(lengths, HQ, HK, D, torch.bfloat16, seed=404)
+    do = torch.randn(q.shape, generator=gen(405)).to(torch.bfloat16).to(DEV)
+    T, scale = q.shape[0], D ** -0.5
+    o = torch.full_like(q, float("nan"))
+    lse = torch.empty((HQ, T), device=DEV)
+    _hip.attn_fwd(q, k, v, o, cu, 1024, scale, lse=lse)
+    dq, dk, dv = (torch.full_like(t, float("nan")) for t in (q, k, v))
+    _hip.attn_bwd(q, k, v, o, do, lse, dq, dk, dv, cu, 1024, scale)
+    q32, k32, v32, do32 = (t.float() for t in (q, k, v, do))
+    want_o = _torch_sdpa(q32, k32, v32, lengths, scale)
+    want = _torch_grads(q32, k32, v32, do32, lengths, scale)
+    for name, got, w in (("o", o, want_o), ("dq", dq, want[0]), ("dk", dk, want[1]),
+                         ("dv", dv, want[2])):
+        g64, w64 = np64(got), np64(w)
+        err = np.abs(g64 - w64)
+        assert np.all(err <= 1e-2 * np.abs(w64).max() + 1e-2 * np.abs(w64) + 1e-5), \
+            (name, float(err.max()), float(np.abs(w64).max()))
