@@ -187,3 +187,28 @@ def test_dx_accumulate_into_buffer():
     summed, da2 = L.lora_down_bwd(x, a16, dxa, key, P, dx_accum=acc.clone())
     assert torch.equal(da1, da2)
     _check(summed, acc.float() + plain.float(), tol=2e-3)
+
+
+def test_dropout_bench_shape():
+    """The bench's dropout workload (config 4's q_proj LoRA input, 8192 x 1536 bf16, p = 0.05:
+    several grid-strided passes per thread): the whole mask bit for bit against the oracle, and
+    the backward's regenerated x_d equal to the forward's."""
+    from solution.body import _hip
+
+    key_v, p = 0x0BAD_5EED_1234_5678, 0.05
+    key = _key(key_v)
+    n = 8192 * 1536
+    x = torch.randn(n, generator=gen(1536)).to(torch.bfloat16).to(DEV)
+    xd = torch.full_like(x, float("nan"))
+    _hip.lora_dropout_fwd(x, key, xd, p)
+    keep = _mask64(key_v, n, p)
+    km = torch.from_numpy(keep).to(DEV)
+    nz = x != 0
+    assert torch.equal((xd != 0) & nz, km & nz)
+    inv = np.float32(1.0) / (np.float32(1.0) - np.float32(p))
+    assert torch.equal(xd[km], (x[km].float() * float(inv)).to(torch.bfloat16))
+    g = torch.randn(n, generator=gen(1537)).to(torch.bfloat16).to(DEV)
+    xd2, dx = torch.empty_like(x), torch.empty_like(x)
+    _hip.lora_dropout_bwd(x, g, key, xd2, dx, p)
+    assert torch.equal(xd2, xd)
+    assert abs(float(keep.mean()) - (1 - p)) < 1e-3

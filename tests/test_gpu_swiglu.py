@@ -122,3 +122,28 @@ def test_recompute_mlp_matches_and_saves_no_intermediate(dtype):
     # a trainable projection sends the block to the non-recompute path
     mlp.up_proj.weight.requires_grad_(True)
     assert packed._mlp_layers(mlp, x) is None
+
+
+def test_swiglu_bench_shape():
+    """The bench's SwiGLU workload (T = 8192 tokens x intermediate 8960, bf16: 73.4M elements,
+    many grid-strided passes per thread): forward and backward on 2^20 sampled elements against
+    the float64 oracle, at the same bar as the small sizes."""
+    from solution.body import _hip
+
+    n = 8192 * 8960
+    g_ = gen(8960)
+    g = (torch.randn(n, generator=g_) * 3).to(torch.bfloat16).to(DEV)
+    u = torch.randn(n, generator=g_).to(torch.bfloat16).to(DEV)
+    dh = torch.randn(n, generator=g_).to(torch.bfloat16).to(DEV)
+    h = torch.full_like(g, float("nan"))
+    _hip.swiglu_fwd(g, u, h)
+    dg, du = torch.full_like(g, float("nan")), torch.full_like(g, float("nan"))
+    _hip.swiglu_bwd(dh, g, u, dg, du)
+    idx = torch.cat([torch.tensor([0, n - 1]), torch.randint(0, n, (1 << 20,), generator=gen(3))]).to(DEV)
+    gs, us, dhs = np64(g[idx]), np64(u[idx]), np64(dh[idx])
+    rt = RTOL[torch.bfloat16]
+    np.testing.assert_allclose(np64(h[idx]), ref.swiglu_fwd(gs, us), rtol=rt, atol=1e-6)
+    dg64, du64 = ref.swiglu_bwd(dhs, gs, us)
+    np.testing.assert_allclose(np64(dg[idx]), dg64, rtol=rt, atol=1e-6)
+    np.testing.assert_allclose(np64(du[idx]), du64, rtol=rt, atol=1e-6)
+    assert not torch.isnan(h).any() and not torch.isnan(dg).any() and not torch.isnan(du).any()
