@@ -273,18 +273,24 @@ int esep_rmsnorm_bwd(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
   a.vec = vec ? 1 : 0;
 
   // The fast kernels (vector rows, one dy, xhat from x, no dr_out). Rows of one wavefront
-  // (n <= 1536) run the pipelined kernel, grid-strided: without a weight gradient on at most
-  // 512 blocks of 4 wavefronts (8 per CU; config 4: 4 rows each, 14.1 us against 15.4 us for
-  // one row per group over 2048 blocks). Wider rows run the wide kernel, one row per group.
+  // (n <= 1536) run the pipelined kernel, grid-strided over at most 256 blocks of 4 wavefronts
+  // without a weight gradient too (one wavefront per SIMD; config 4: 8 rows each, 14.3 us,
+  // against 14.7 us on 512 blocks). Wider rows run the wide kernel, one row per group.
   const int threads = gpb * 64 * wpr;
   const bool plain = vec && n_dy == 1 && !from_y && dr_out == nullptr && n_special == 0;
-  a.fast = 0;
-  if (plain && wpr == 1 && threads <= esep::kBwdPipeThreads && rows < (int64_t{1} << 30))
-    a.fast = 1;  // 32-bit row indices
-  else if (plain)
-    a.fast = 2;
   int64_t blocks = part ? bwd_partials(rows, n) : (rows + gpb - 1) / gpb;
-  if (!part && a.fast == 1 && blocks > 512) blocks = 512;
+  // The pipelined kernel's grid: the partials' P blocks, or at most 256 without them. It takes at
+  // most 64 rows per row group (one saved-rstd vector load); longer runs go to the wide kernel,
+  // whose grid-strided rows and fixed-order block sums give the same partials bit for bit.
+  const int64_t pipe_blocks = (!part && blocks > 256) ? 256 : blocks;
+  const int64_t rows_per_group = (rows + pipe_blocks * gpb - 1) / (pipe_blocks * gpb);
+  a.fast = 0;
+  if (plain && wpr == 1 && threads == esep::kBwdPipeThreads && rows_per_group <= 64) {
+    a.fast = 1;
+    blocks = pipe_blocks;
+  } else if (plain) {
+    a.fast = 2;
+  }
   if (blocks > 0x7fffffff) return fail(ESEP_ESHAPE, "rmsnorm_bwd: too many rows");
   // LDS. The pipelined kernel keeps, with a weight gradient, one slot of nv * 64 * 8 floats per
   // row group for the block sum (4 groups: 24 KiB). The wide kernel also stages the weight

@@ -470,35 +470,56 @@ __device__ __forceinline__ void bwd_rows(const BwdArgs& a, float* red, float* ld
   if (want_dw) dw_block_partial<NV, VEC>(a, acc, lds, grp, gpb, tg, G);
 }
 
+// The pipelined backward runs blocks of 4 wavefronts (one row group each), one block per CU at
+// config-4 sizes, so each wavefront may hold up to 512 registers without lowering occupancy.
+constexpr int kBwdPipeThreads = 256;
+
 // Fast backward for the common call (one gradient of y, xhat from x, not from y, no dr_out,
-// 16-byte-aligned whole chunks) on rows of one wavefront (n <= 1536). Rows are grid-strided (row group g of block b takes rows
-// (b + i * P) * gpb + g) and software-pipelined: two register sets with fixed roles hold the
-// raw (still packed) dy and x of two rows, and row i + 1's loads are issued before row i is
-// computed and stored. The sets alternate by loop unrolling, never by copying: a copy of a
-// prefetched register would wait for its load and serialize the rows again. Each lane always
-// owns the same columns, so its weight chunks (NV * 8 floats) are loaded once into registers
-// (no LDS staging, no barrier before the first row). With a weight gradient, each lane sums
-// dy * xhat of its chunks in registers over its group's rows; at the end the groups park their
-// sums in one LDS slot each (NV * G * 8 floats) and the block adds the slots in group order
-// into its row of the [P, n] partials.
+// 16-byte-aligned whole chunks) on rows of one wavefront (n <= 1536). Rows are grid-strided (row
+// group g of block b takes rows (b + i * P) * gpb + g, so the rows in flight at any moment are
+// one contiguous stretch of memory).
+//
+// Schedule. Two register sets with fixed roles hold the raw (still packed) dy and x of two
+// rows: row i is computed from set i % 2, then row i + 2's loads are issued into the same set,
+// then row i's dx is stored. Scheduling barriers pin that order (the compiler otherwise sinks
+// the next row's loads into the middle of the current row's arithmetic, which leaves about one
+// row in flight). The loads of row i + 1 are thus always in flight while row i is computed,
+// and the stores are issued after the loads they follow, so no wait for a row's data ever
+// waits for a store (gfx9's vmcnt counts loads and stores in one in-order counter). Row 0 is
+// peeled off and the last row is kept out of the loop, so the loop is entered with the same
+// outstanding operations as it loops back with and its waits stay exact. Each lane owns the same
+// columns of every row, so its weight chunks (NV * 8 floats) are loaded once into registers.
+// The saved rstd of the group's rows comes in one vector load and is read per row with readlane;
+// the entry point sends inputs of more than 64 rows per group to the wide kernel.
+//
+// Weight gradient: each lane sums dy * xhat of its chunks in registers over its group's rows;
+// after the last row the groups park their sums in one LDS slot each (NV * G * 8 floats, indexed
+// by column) and, after one barrier, every thread adds the slots of column pairs 2t, 2t + 2 *
+// threads, ... in group order and stores them (non-temporal) as the block's row of the [P, n]
+// partials.
+//
+// Measured at config 4 (8192 x 1536 bf16, 256 blocks of 4 wavefronts, graphs of 57 launches):
+// 15.19 us with the compiler's placement (a full wait at the loop head, one row in flight),
+// 14.9 us pinned. Ablations of the pinned kernel: no arithmetic (a raw copy of the same rows)
+// 13.7 us, arithmetic without the partials' store 14.3 us.
+//
 // FIX fixes the call's optional parts at compile time: 1 = saved rstd, dx only, with the weight
-// gradient; 2 = the same without it; 0 reads them from the arguments. The fixed forms have no
-// branch in the row loop and none of the register copies the branches' joins cost (config 4:
-// 15.36 -> 15.12 us with the weight gradient, 14.7 -> 14.2 us without).
+// gradient; 2 = the same without it; 0 reads them from the arguments.
 template <int NV, typename TX, typename TDY, typename TO, int FIX>
 __device__ __forceinline__ void bwd_rows_pipe(const BwdArgs& a, float* lds) {
   constexpr int G = kWave;  // one wavefront per row: every row reduction is a DPP wave sum
-  const int gpb = a.gpb;  // blockDim.x would cost a vector load of the hidden kernel arguments
+  constexpr int gpb = kBwdPipeThreads / kWave;  // the launch is checked to match
   const int grp = wave_id();
   const int tg = (int)threadIdx.x & (kWave - 1);
   const int lane = tg;
   const int n = a.n;
-  // 32-bit scalar row indices (the entry point sends rows < 2^31 here): scalar compares, no
-  // 64-bit vector compare per row
+  // 32-bit scalar row indices (the entry point sends rows < 2^30 here)
   const int rows = (int)a.rows;
   const int step = (int)gridDim.x * gpb;  // grid-strided rows
   const int first = (int)blockIdx.x * gpb + grp;
-  const int iters = (rows - first + step - 1) / step;  // rows of this group (block-uniform count)
+  const int iters = (rows - first + step - 1) / step;  // rows of this group
+  // rows of the block's groups (block-uniform: the groups of a block differ by at most one row;
+  // a group's surplus rows read 0 and store nothing), at least 1
   const int iters_blk = (rows - (int)blockIdx.x * gpb + step - 1) / step;
   const bool want_dw = FIX == 1 ? true : FIX == 2 ? false : a.part != nullptr;
   const bool has_rstd = FIX != 0 || a.rstd != nullptr;
@@ -512,8 +533,7 @@ __device__ __forceinline__ void bwd_rows_pipe(const BwdArgs& a, float* lds) {
 #pragma unroll
     for (int k = 0; k < NV; ++k) bload<true, float, kCached>(rw, (tg + k * G) * 32, wr[k]);
   }
-  // Saved rstd of this group's rows it0 .. it0 + 63: lane l holds row first + (it0 + l) * step,
-  // read per row with readlane (one load per 64 rows, none in the row loop).
+  // Saved rstd of this group's rows (at most 64): lane l holds row first + l * step.
   float rstd64 = 1.f;
   auto load_rstd = [&](int it0) {
     if (has_rstd) {
@@ -521,13 +541,13 @@ __device__ __forceinline__ void bwd_rows_pipe(const BwdArgs& a, float* lds) {
       rstd64 = it < iters ? a.rstd[first + (int64_t)it * step] : 1.f;
     }
   };
-  load_rstd(0);
 
   Raw<TDY> rdy[2][NV];
   Raw<TX> rx[2][NV];
-  // Loads of one row into register set `set`; a row past the end gets 0-byte buffers (its
-  // loads read 0 without touching memory).
-  auto fetch = [&](int set, int row) {
+  // Loads of row `it` of this group into register set `set`; a row past the end gets 0-byte
+  // buffers (its loads read 0 without touching memory).
+  auto fetch = [&](int set, int it) {
+    const int row = first + it * step;
     const bool ok = row < rows;
     const Span sd = row_rsrc<TDY>(a.dy[0], row, a.ld_dy, n, ok);
     const Span sx = row_rsrc<TX>(a.x, row, a.ld_x, n, ok);
@@ -544,11 +564,10 @@ __device__ __forceinline__ void bwd_rows_pipe(const BwdArgs& a, float* lds) {
 #pragma unroll
     for (int e = 0; e < 8; ++e) dwa[k][e] = 0.f;
 
-  // Row `it` of this group from register set `set`:
+  // Row `it` of this group from register set `set` into o:
   // dx = rstd * (g - xhat * mean(g * xhat)), g = dy * w.
-  auto finish = [&](int set, int it) {
-    const int row = first + it * step;
-    const bool ok = row < rows;  // a row that does not exist has dy = x = 0: adds nothing
+  float o[NV][8];
+  auto compute = [&](int set, int it) {
     float dy[NV][8], x[NV][8];
 #pragma unroll
     for (int k = 0; k < NV; ++k) {
@@ -588,36 +607,55 @@ __device__ __forceinline__ void bwd_rows_pipe(const BwdArgs& a, float* lds) {
 #pragma unroll
     for (int k = 0; k < NV; ++k)
 #pragma unroll
-      for (int e = 0; e < 8; ++e) dy[k][e] = inv * (dy[k][e] - x[k][e] * proj);
+      for (int e = 0; e < 8; ++e) o[k][e] = inv * (dy[k][e] - x[k][e] * proj);
+  };
+  auto store = [&](int it) {
+    const int row = first + it * step;
+    const bool ok = row < rows;  // a row that does not exist has dy = x = 0: adds nothing
     if (has_dr) {
       const Span so = row_rsrc<float>(a.dr, row, a.ld_out, n, ok);
 #pragma unroll
-      for (int k = 0; k < NV; ++k) bstore<true, float>(so, (tg + k * G) * 32, dy[k]);
+      for (int k = 0; k < NV; ++k) bstore<true, float>(so, (tg + k * G) * 32, o[k]);
     }
     if (has_dx) {
       const Span so = row_rsrc<TO>(a.dx, row, a.ld_out, n, ok);
 #pragma unroll
-      for (int k = 0; k < NV; ++k) bstore<true, TO>(so, (tg + k * G) * 8 * sizeof(TO), dy[k]);
+      for (int k = 0; k < NV; ++k) bstore<true, TO>(so, (tg + k * G) * 8 * sizeof(TO), o[k]);
     }
   };
+  // row `it` from `set`, then row it + 2 into the same set, then row it's stores
+  auto finish = [&](int set, int it) {
+    compute(set, it);
+    __builtin_amdgcn_sched_barrier(0);
+    fetch(set, it + 2);
+    __builtin_amdgcn_sched_barrier(0);
+    store(it);
+  };
 
-  // Two rows per pass with both register sets always consumed (an odd last row is peeled off
-  // after the loop): no path reaches the loop head with a set's loads still in flight, so the
-  // compiler's waits stay on the row being finished. The pass count is the block's (the
-  // groups of a block differ by at most one row; a group's surplus rows read 0 and store
-  // nothing).
-  fetch(0, first);
-  int it = 0;
-  for (; it + 2 <= iters_blk; it += 2) {
-    if (it != 0 && (it & (kWave - 1)) == 0) load_rstd(it);
-    fetch(1, first + (it + 1) * step);
-    finish(0, it);
-    fetch(0, first + (it + 2) * step);
-    finish(1, it + 1);
-  }
-  if (it < iters_blk) {
-    if (it != 0 && (it & (kWave - 1)) == 0) load_rstd(it);
-    finish(0, it);
+  // The two-set pipeline over this group's rows 0 .. iters_blk - 1 (at most 64, one saved-rstd
+  // window: the entry point sends longer runs to the wide kernel).
+  load_rstd(0);
+  fetch(0, 0);
+  fetch(1, 1);
+  __builtin_amdgcn_sched_barrier(0);
+  if (iters_blk == 1) {
+    compute(0, 0);
+    store(0);
+  } else {
+    finish(0, 0);
+    int it = 1;  // rows it (set 1) and it + 1 (set 0) per pass; the last row after the loop
+    for (; it + 2 < iters_blk; it += 2) {
+      finish(1, it);
+      finish(0, it + 1);
+    }
+    if (it + 1 < iters_blk) {
+      finish(1, it);
+      compute(0, it + 1);
+      store(it + 1);
+    } else {
+      compute(1, it);
+      store(it);
+    }
   }
 
   if (want_dw) {
@@ -625,21 +663,29 @@ __device__ __forceinline__ void bwd_rows_pipe(const BwdArgs& a, float* lds) {
     float* acc = lds + grp * stride;
 #pragma unroll
     for (int k = 0; k < NV; ++k) Chunk<float>::store(acc + 8 * (tg + k * G), dwa[k]);
-    // block sum: column quads over all threads, groups added in group order
-    __syncthreads();
-    float* dst = a.part + (int64_t)blockIdx.x * n;
-    for (int q = threadIdx.x; 4 * q < n; q += gpb * G) {
-      f32x4 t = *reinterpret_cast<const f32x4*>(lds + 4 * q);
-      for (int g = 1; g < gpb; ++g) t += *reinterpret_cast<const f32x4*>(lds + g * stride + 4 * q);
-      *reinterpret_cast<f32x4*>(dst + 4 * q) = t;
+    __syncthreads();  // LDS only: on gfx950 this waits for LDS writes, not for the dx stores
+    // block sum of column pairs 2t, 2t + 2 * threads, ..., groups added in group order
+    const rsrc_t rp = make_rsrc(a.part + (int64_t)blockIdx.x * n, (uint32_t)n * 4u);
+    constexpr int nthr = gpb * G;
+#pragma unroll
+    for (int j = 0; j < (NV * G * 8) / (2 * nthr); ++j) {
+      const int c = 2 * (int)threadIdx.x + 2 * nthr * j;
+      if (c < n) {
+        float2 t = *reinterpret_cast<const float2*>(lds + c);
+#pragma unroll
+        for (int g = 1; g < gpb; ++g) {
+          const float2 u = *reinterpret_cast<const float2*>(lds + g * stride + c);
+          t.x += u.x;
+          t.y += u.y;
+        }
+        typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+        __builtin_amdgcn_raw_buffer_store_b64(u32x2{__float_as_uint(t.x), __float_as_uint(t.y)},
+                                              rp, (uint32_t)c * 4u, 0, kStream);
+      }
     }
   }
 }
 
-// The pipelined backward's kernel: at most 512 threads, so each wavefront may hold up to 256
-// VGPRs (two register sets of raw rows, the weight chunks and the weight-gradient sums; 120 to
-// 220 with the element types) without spilling.
-constexpr int kBwdPipeThreads = 512;
 template <int NV, typename TX, typename TDY, typename TO, int FIX>
 __global__ __launch_bounds__(kBwdPipeThreads) void k_rmsnorm_bwd_pipe(const BwdArgs a) {
   extern __shared__ float lds[];

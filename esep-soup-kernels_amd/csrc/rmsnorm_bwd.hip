@@ -20,7 +20,8 @@ static hipError_t bwd_nv(const BwdArgs& a, int nv, dim3 grid, dim3 block, size_t
   // launch shape.
   const bool fast = a.fast != 0;
   if (a.fast == 1) {
-    if (block.x > (unsigned)kBwdPipeThreads || a.wpr != 1) return hipErrorInvalidValue;
+    if (block.x != (unsigned)kBwdPipeThreads || a.gpb != kBwdPipeThreads / kWave || a.wpr != 1)
+      return hipErrorInvalidValue;
     // saved rstd and dx only (the common call) run a form with those parts fixed
     const bool common = a.rstd != nullptr && a.dr == nullptr && a.dx != nullptr;
     const int fix = common ? (a.part != nullptr ? 1 : 2) : 0;

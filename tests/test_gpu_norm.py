@@ -401,11 +401,11 @@ def test_rmsnorm_dx_independent_of_weight_grad(dtype, n, recompute):
 
 @pytest.mark.parametrize("n", [64, 1536])
 def test_rmsnorm_bwd_many_rows_per_wavefront(n):
-    """Past 64 rows per wavefront the pipelined backward reloads its window of saved rstd values
-    (one vector load per 64 rows): 150000 rows of 64 columns give ~147 rows per wavefront with
-    the weight gradient (256 blocks) and ~73 without it (512 blocks); 40000 rows of 1536 give
-    ~39 and ~20. dx on rows from every window and dw against the fp64 oracle, and dx the same
-    bits with and without the weight gradient."""
+    """Past 64 rows per wavefront (one vector load of saved rstd values) the entry point sends the
+    call from the pipelined backward to the wide one: 150000 rows of 64 columns give ~147 rows
+    per wavefront on 256 blocks, with and without the weight gradient; 40000 rows of 1536 give
+    ~39 (the pipelined kernel). dx on rows spread over the input and dw against the fp64 oracle,
+    and dx the same bits with and without the weight gradient."""
     nr = _nr()
     g = gen(77 + n)
     T = 150000 if n == 64 else 40000
