@@ -21,8 +21,9 @@ each required tensor once (e = 2 bytes):
 With --rstd recomputed the 4T terms go away (rstd is recomputed from x in backward).
 
 Also printed: the roofline of the dominant kernel (per-launch HIP-event timing of graphs of
-that kernel alone, on the stream it runs on); the streaming ceiling (esep_stream_probe at each
-kernel's bytes and launch pattern, and the step those launches would take); configs 1-3
+that kernel alone, on the stream it runs on); the streaming ceiling (the fastest of the bench's
+streaming probes, benchlib/probe.hip, at each kernel's bytes and launch pattern, and the step
+built of those probes, timed); configs 1-3
 (cache-resident and with the Infinity Cache flushed); config 5; the neighbours' kernels; and
 the CPU baseline: the PyTorch-eager fp32 restatement of HF's Qwen2RMSNorm / rotary path
 (oracle/hf_eager.py) timed on this host's cores on one layer of the same workload.
@@ -286,15 +287,52 @@ def run_config4_per_call_dgamma(dev, steps, save_rstd):
             "launches_per_step": 4 * CFG4["layers"] + 2 + 2 * CFG4["layers"] + 1 + 2 * CFG4["layers"] + 1 - 1}
 
 
-def stream_ceiling(dev, cfg, kernel_us, reps):
-    """Per-launch ceiling of one streaming launch at each path kernel's own byte counts and
-    launch pattern: esep_stream_probe (one or two streams read, one written; grid-strided,
-    non-temporal) in a graph of one launch per layer over distinct buffers, the best of three
-    grid sizes, beside the kernel's own per-launch time. Also the step those probes would
-    take with the step's launch counts (a step of pure streaming launches)."""
-    import torch
+# Streaming probes (benchlib/libesep_probe.so): one-shot grids with U = 1, 2, 4, 8 chunks of 16
+# bytes per stream per lane, and fixed strided grids with the next step's U chunks issued before
+# this step's stores (2U in flight), over 256 to 2048 blocks.
+PROBE_VARIANTS = ([("oneshot", u, t, 1) for u in (1, 2, 4, 8) for t in (256, 512)]
+                  + [("strided", u, t, b) for u, t in ((1, 512), (2, 512), (4, 256), (4, 512), (8, 256))
+                     for b in (256, 512, 1024, 2048)])
 
-    from solution.body import _hip
+
+def _probe_launch(variant, bufs, n_src):
+    import benchlib
+
+    mode, u, t, blocks = variant
+    m = benchlib.ONESHOT if mode == "oneshot" else benchlib.STRIDED
+    benchlib.stream(bufs[0], bufs[-1], bufs[1] if n_src == 2 else None, mode=m, u=u, threads=t,
+                    blocks=blocks)
+
+
+def _probe_sweep(bufsets, n_src, reps):
+    """Per-launch microseconds of every probe variant over the launches of bufsets (one graph of
+    one launch per buffer set), fastest first."""
+    res = []
+    for v in PROBE_VARIANTS:
+        def fn(v=v):
+            for bs in bufsets:
+                _probe_launch(v, bs, n_src)
+        gr = capture(fn)
+        time_graph(gr, 2)
+        ms, _ = time_graph(gr, reps)
+        res.append((ms * 1e3 / len(bufsets), v))
+        del gr
+    return sorted(res)
+
+
+def _vname(v):
+    mode, u, t, b = v
+    return f"{mode} U{u} x {t} threads" + ("" if mode == "oneshot" else f", {b} blocks")
+
+
+def stream_ceiling(dev, cfg, kernel_us, reps, step_ms):
+    """The streaming ceiling of each path kernel: every probe variant at that kernel's own byte
+    counts (one or two streams read, one written) and launch pattern (a graph of one launch per
+    layer over distinct buffers), the fastest kept, beside the kernel's per-launch time. Then the
+    step itself built of those fastest probes: the step's 170 path launches in the step's order,
+    each replaced by its kernel's best probe over buffers of its own, captured in one graph and
+    timed like the step (no weight-gradient stage 2: its partials are not algorithmic bytes)."""
+    import torch
 
     T, H, HQ, HK, D, L = (cfg[k] for k in ("T", "H", "HQ", "HK", "D", "layers"))
     e = 2
@@ -304,66 +342,82 @@ def stream_ceiling(dev, cfg, kernel_us, reps):
         "rope_fwd": (1, e * T * (HQ + HK) * D, L),
         "rope_bwd": (1, e * T * (HQ + HK) * D, L),
     }
-    out, probe_cache = {}, {}
+    bufs = {name: [[torch.empty(nbytes, device=dev, dtype=torch.uint8) for _ in range(n_src + 1)]
+                   for _ in range(launches)]
+            for name, (n_src, nbytes, launches) in kinds.items()}
+    out, best = {}, {}
     for name, (n_src, nbytes, launches) in kinds.items():
-        key = (n_src, nbytes, launches)
-        if key not in probe_cache:
-            bufs = [[torch.empty(nbytes, device=dev, dtype=torch.uint8) for _ in range(n_src + 1)]
-                    for _ in range(launches)]
-            best = None
-            for blocks in (512, 1024, 2048):
-                def fn(blocks=blocks):
-                    for b in bufs:
-                        _hip.stream_probe(b[0], b[-1], b[1] if n_src == 2 else None, blocks=blocks)
-                gr = capture(fn)
-                time_graph(gr, 2)
-                ms, _ = time_graph(gr, reps)
-                us = ms * 1e3 / launches
-                if best is None or us < best[0]:
-                    best = (us, blocks)
-                del gr
-            del bufs
-            torch.cuda.empty_cache()
-            probe_cache[key] = best
-        us, blocks = probe_cache[key]
+        res = _probe_sweep(bufs[name], n_src, reps)
+        us, v = res[0]
+        best[name] = v
         algo = (n_src + 1) * nbytes
         k_us = kernel_us.get(name)
-        out[name] = {"probe_us": round(us, 3), "probe_blocks": blocks,
+        out[name] = {"probe_us": round(us, 3), "probe": _vname(v),
                      "probe_GB/s": round(algo / (us * 1e-6) / 1e9, 1), "launches_per_step": launches,
+                     "runners_up": [{"us": round(u2, 3), "probe": _vname(v2)} for u2, v2 in res[1:4]],
                      "kernel_us": None if k_us is None else round(k_us, 3),
                      "kernel_over_probe": None if k_us is None else round(k_us / us, 4)}
-        log(f"stream ceiling {name}: probe {us:.2f} us ({blocks} blocks), kernel "
+        log(f"stream ceiling {name}: best probe {us:.2f} us ({_vname(v)}), kernel "
             f"{k_us if k_us is None else round(k_us, 2)} us")
-    step_ms = sum(v["probe_us"] * v["launches_per_step"] for v in out.values()) * 1e-3
+
+    def probe_step():
+        nf = lambda i: _probe_launch(best["rmsnorm_fwd"], bufs["rmsnorm_fwd"][i], 1)
+        nb = lambda i: _probe_launch(best["rmsnorm_bwd"], bufs["rmsnorm_bwd"][i], 2)
+        rf = lambda l: _probe_launch(best["rope_fwd"], bufs["rope_fwd"][l], 1)
+        rb = lambda l: _probe_launch(best["rope_bwd"], bufs["rope_bwd"][l], 1)
+        for l in range(L):
+            nf(2 * l)
+            rf(l)
+            nf(2 * l + 1)
+        nf(2 * L)
+        nb(2 * L)
+        for l in reversed(range(L)):
+            nb(2 * l + 1)
+            rb(l)
+            nb(2 * l)
+    gr = capture(probe_step)
+    time_graph(gr, 3)
+    ev_ms, wall_ms = time_graph(gr, 20)
+    pstep = max(ev_ms, wall_ms)
+    del gr, bufs
+    torch.cuda.empty_cache()
+    sum_ms = sum(v["probe_us"] * v["launches_per_step"] for v in out.values()) * 1e-3
     floor = launch_floor(dev, cfg, kinds, reps)
-    return {"what": "esep_stream_probe (out = a (+ b)) at each kernel's bytes and launch pattern, "
-                    "best of 512/1024/2048 blocks of 512 threads",
-            "kernels": out, "probe_step_ms": round(step_ms, 4), "floor": floor}
+    step_bytes = sum((n_src + 1) * nbytes * launches for n_src, nbytes, launches in kinds.values())
+    log(f"probe step {pstep:.3f} ms ({step_bytes / (pstep * 1e-3) / 1e9:.0f} GB/s); kernel step "
+        f"{step_ms:.3f} ms")
+    return {"what": "benchlib probes (out = a (+ b), non-temporal 16-byte buffer loads and stores) "
+                    f"at each kernel's bytes and launch pattern, fastest of {len(PROBE_VARIANTS)} "
+                    "variants: one-shot grids with 1/2/4/8 chunks per stream per lane (256 or 512 "
+                    "threads), strided grids of 256-2048 blocks with 1-8 chunks per stream per lane "
+                    "and the next step's chunks issued before this step's stores",
+            "kernels": out,
+            "probe_step_ms": round(pstep, 4),
+            "probe_step_GB/s": round(step_bytes / (pstep * 1e-3) / 1e9, 1),
+            "probe_step_frac_of_peak": round(step_bytes / (pstep * 1e-3) / 1e9 / PEAK_GBS, 4),
+            "probe_sum_ms": round(sum_ms, 4),
+            "step_ms": round(step_ms, 4),
+            "step_over_probe_step": round(step_ms / pstep, 4),
+            "floor": floor}
 
 
 def launch_floor(dev, cfg, kinds, reps):
     """The fixed cost of the step's launch structure, measured in the same run:
-      launch_us     the time per launch of a graph of 57 nearly empty launches (esep_stream_probe
-                    over 16 bytes, one block): what each dependent launch costs before any data
-                    moves (the command processor's end-of-kernel and dispatch work);
+      launch_us     the time per launch of a graph of 57 nearly empty launches (a probe over 16
+                    bytes, one block): what each dependent launch costs before any data moves
+                    (the command processor's end-of-kernel and dispatch work);
       launch_ms     launch_us times the step's launches (time no kernel design removes while
                     every op is its own launch);
       asymptote     the rate of one streaming launch over 1 GiB per stream (1 read + 1 write,
-                    2 reads + 1 write), best of 1024 / 2048 / 4096 blocks. It is below the
-                    per-launch rates at config 4's 25-75 MB sizes, whose writes the 256 MB
-                    Infinity Cache absorbs and writes back during later launches, so it bounds
-                    nothing here; it is reported for the record."""
+                    2 reads + 1 write), fastest probe variant."""
     import torch
 
-    from solution.body import _hip
-
     n = 57
-    tiny = [(torch.empty(16, device=dev, dtype=torch.uint8), torch.empty(16, device=dev, dtype=torch.uint8))
-            for _ in range(n)]
+    tiny = [[torch.empty(16, device=dev, dtype=torch.uint8) for _ in range(2)] for _ in range(n)]
 
     def empties():
-        for a, o in tiny:
-            _hip.stream_probe(a, o, blocks=1)
+        for bs in tiny:
+            _probe_launch(("strided", 1, 256, 1), bs, 1)
     gr = capture(empties)
     time_graph(gr, 2)
     ms, _ = time_graph(gr, reps)
@@ -371,20 +425,14 @@ def launch_floor(dev, cfg, kinds, reps):
     del gr, tiny
 
     big = 1 << 30
-    rates = {}
+    rates, names = {}, {}
     bufs = [torch.empty(big, device=dev, dtype=torch.uint8) for _ in range(3)]
     for n_src in (1, 2):
-        best = None
-        for blocks in (1024, 2048, 4096):
-            def fn(blocks=blocks):
-                _hip.stream_probe(bufs[0], bufs[2], bufs[1] if n_src == 2 else None, blocks=blocks)
-            gr = capture(fn)
-            time_graph(gr, 1)
-            ms, _ = time_graph(gr, 5)
-            gbs = (n_src + 1) * big / (ms * 1e-3) / 1e9
-            best = gbs if best is None or gbs > best else best
-            del gr
-        rates[n_src] = best
+        res = _probe_sweep([[bufs[0], bufs[1], bufs[2]] if n_src == 2 else [bufs[0], bufs[2]]],
+                           n_src, 3)
+        us, v = res[0]
+        rates[n_src] = (n_src + 1) * big / (us * 1e-6) / 1e9
+        names[n_src] = _vname(v)
     del bufs
     torch.cuda.empty_cache()
     launches = sum(v[2] for v in kinds.values()) + 1  # + the batched weight-gradient reduce
@@ -392,7 +440,8 @@ def launch_floor(dev, cfg, kinds, reps):
         f"asymptotes 1R1W {rates[1]:.0f} / 2R1W {rates[2]:.0f} GB/s")
     return {"launch_us": round(launch_us, 3), "launches_per_step": launches,
             "launch_ms": round(launches * launch_us * 1e-3, 4),
-            "asymptote_GB/s": {"1R1W": round(rates[1], 1), "2R1W": round(rates[2], 1)}}
+            "asymptote_GB/s": {"1R1W": round(rates[1], 1), "2R1W": round(rates[2], 1)},
+            "asymptote_probe": {"1R1W": names[1], "2R1W": names[2]}}
 
 
 def _flush_buffer(dev):
@@ -1236,9 +1285,7 @@ def main():
     del g
     del body
     torch.cuda.empty_cache()
-    ceiling = stream_ceiling(dev, c4dims, {k: v[0] for k, v in kr.items()}, args.kernel_reps)
-    ceiling["step_ms"] = round(ms, 4)
-    ceiling["step_over_probe_step"] = round(ms / ceiling["probe_step_ms"], 4)
+    ceiling = stream_ceiling(dev, c4dims, {k: v[0] for k, v in kr.items()}, args.kernel_reps, ms)
     small = run_small_configs(dev, args.kernel_reps)
     c4_other = run_config4_other_rstd(dev, max(args.steps // 3, 5), not save_rstd)
     c4_per_call = run_config4_per_call_dgamma(dev, max(args.steps // 3, 5), save_rstd)

@@ -107,11 +107,6 @@ int attn_split(int64_t T, int HQ, int HK) {
 
 }  // namespace
 
-namespace esep {
-hipError_t launch_stream_probe(const void* a, const void* b, void* out, int64_t bytes, int blocks,
-                               hipStream_t s);
-}
-
 extern "C" {
 
 int esep_abi_version(void) { return ESEP_ABI_VERSION; }
@@ -793,22 +788,6 @@ int esep_head_row_softmax(void* z, int64_t ld, const int64_t* target, const floa
       esep::launch_head_row(a, dt, vec, static_cast<hipStream_t>(stream), &sup);
   if (!sup) return fail(ESEP_EINVAL, "head_row_softmax: unsupported dtype");
   return e == hipSuccess ? 0 : hip_fail(e, "head_row_softmax launch");
-}
-
-int esep_stream_probe(const void* a, const void* b, void* out, int64_t bytes, int blocks,
-                      void* stream) {
-  g_err[0] = 0;
-  if (a == nullptr || out == nullptr)
-    return fail(ESEP_EINVAL, "stream_probe: a and out are required");
-  if (!aligned16(a) || !aligned16(out) || (b != nullptr && !aligned16(b)))
-    return fail(ESEP_EALIGN, "stream_probe: buffers must be 16-byte aligned");
-  if (bytes < 0 || (bytes & 15) != 0 || blocks < 1 || blocks > (1 << 20))
-    return fail(ESEP_ESHAPE, "stream_probe: bytes=%lld must be a multiple of 16, blocks=%d in "
-                "[1, 2^20]", (long long)bytes, blocks);
-  if (bytes == 0) return 0;
-  const hipError_t e = esep::launch_stream_probe(a, b, out, bytes, blocks,
-                                                 static_cast<hipStream_t>(stream));
-  return e == hipSuccess ? 0 : hip_fail(e, "stream_probe launch");
 }
 
 }  // extern "C"

@@ -60,7 +60,6 @@ SIGNATURES = {
     "esep_attn_bwd": (_i32, [_vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _i64, _vp, _vp,
                              _vp, _i64, _vp, _i64, _vp, _i64, _i32, _i64, _i32, _i32, _i32, _vp,
                              _i32, _i32, _f32, _vp]),
-    "esep_stream_probe": (_i32, [_vp, _vp, _vp, _i64, _i32, _vp]),
     "esep_rope": (_i32, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i32, _i64, _i64,
                          _i32, _i32, _i32, _vp, _i32, _vp, _vp, _i32, _vp, _f32, _vp]),
 }
@@ -552,19 +551,4 @@ def head_row_softmax(z, target, cew, lse, tlogit, ent, amax, write_g, g_scale,
                                      _p(amax), rows, V, 1 if write_g else 0, float(g_scale),
                                      dtype_code(z.dtype), _stream(dev))
     _check(rc, "esep_head_row_softmax")
-    _record(name)
-
-
-def stream_probe(a, out, b=None, blocks=1024, name="_stream_probe"):
-    """out = a (+ b) over the bytes of out (esep_stream_probe): the streaming ceiling bench.py
-    compares the path kernels with. Contiguous tensors of out's byte size."""
-    dev = _dev(a, b, out)
-    nbytes = out.numel() * out.element_size()
-    for t in (a, b):
-        if t is not None and (not t.is_contiguous() or t.numel() * t.element_size() != nbytes):
-            raise EsepError("stream_probe inputs must be contiguous and as large as out")
-    if not out.is_contiguous():
-        raise EsepError("stream_probe out must be contiguous")
-    rc = lib().esep_stream_probe(_p(a), _p(b), _p(out), nbytes, int(blocks), _stream(dev))
-    _check(rc, "esep_stream_probe")
     _record(name)

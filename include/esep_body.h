@@ -183,17 +183,6 @@ int esep_dgamma_reduce_batch(const esep_dgamma_item* items, int n_items, int64_t
                              void* stream);
 
 /*
- * Measurement only (no reference counterpart; not on the decoder path): out = a (+ b) over
- * `bytes` bytes as 32-bit lanes, one grid-strided streaming pass of `blocks` blocks of 512
- * threads (non-temporal 16-byte loads and stores). bench.py times it at each path kernel's own
- * byte counts as the rate a single streaming launch of that size reaches (the per-launch
- * ceiling the kernels are compared with). a, b (or NULL), out: 16-byte aligned device buffers
- * of `bytes` bytes (a multiple of 16); 1 <= blocks <= 2^20.
- */
-int esep_stream_probe(const void* a, const void* b, void* out, int64_t bytes, int blocks,
-                      void* stream);
-
-/*
  * Rotary embedding on q and k in one launch (forward with sin_sign = +1, backward with -1).
  * Replaces the launch of _rope_kernel at solution/body/norm_rope.py:388-392 (_launch_rope);
  * kernel math follows norm_rope.py:330-369 (rotate_half convention of HF apply_rotary_pos_emb).

@@ -268,14 +268,3 @@ def test_apply_installs_the_patches_idempotently():
     finally:
         mq.Qwen2MLP.forward, mq.Qwen2Model.forward = mlp0, model0
 
-
-def test_stream_probe_validation():
-    """The measurement entry point checks pointers, alignment and sizes before launching."""
-    lib = _hip.lib()
-    assert lib.esep_stream_probe(None, None, 64, 64, 1, None) == -1
-    assert lib.esep_stream_probe(64, None, 72, 64, 1, None) == -3
-    assert lib.esep_stream_probe(64, 8, 64, 64, 1, None) == -3
-    assert lib.esep_stream_probe(64, None, 64, 40, 1, None) == -2
-    assert lib.esep_stream_probe(64, None, 64, 64, 0, None) == -2
-    assert lib.esep_stream_probe(64, None, 64, 0, 1, None) == 0  # nothing to stream
-

@@ -3,9 +3,7 @@ keeps every trainable norm's [P, n] partials and reduces all of them in one
 esep_dgamma_reduce_batch launch at the end of the pass, then accumulates into .grad. The
 gradients must be the bits of the per-call reduction (the batched reduce sums each norm's
 partials in the same order), and every case where deferral cannot see the gradient's consumer
-(autograd.grad, backward(inputs=...), hooks, create_graph) must take the per-call path.
-
-Also: the streaming measurement kernel (esep_stream_probe) computes out = a (+ b)."""
+(autograd.grad, backward(inputs=...), hooks, create_graph) must take the per-call path."""
 
 import numpy as np
 import pytest
@@ -172,16 +170,3 @@ def test_deferred_inside_graph_capture_replays():
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(captured, eager)
-
-
-@pytest.mark.parametrize("two", [False, True])
-def test_stream_probe_values(two):
-    from solution.body import _hip
-
-    g = torch.Generator(device=DEV).manual_seed(7)
-    a = torch.randint(0, 1 << 30, (1 << 20,), generator=g, device=DEV, dtype=torch.int32)
-    b = torch.randint(0, 1 << 30, (1 << 20,), generator=g, device=DEV, dtype=torch.int32) if two else None
-    out = torch.empty_like(a)
-    _hip.stream_probe(a, out, b, blocks=300)
-    want = a + b if two else a
-    assert torch.equal(out, want)
