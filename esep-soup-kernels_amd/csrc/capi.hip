@@ -370,6 +370,19 @@ int esep_rmsnorm_bwd_noalloc(const void* const* dys, int n_dy, int dy_dt, int64_
     return fail(ESEP_ESHAPE, "rmsnorm_bwd_noalloc: %lld x %lld partials exceed the %lld-float "
                 "scratch (use esep_rmsnorm_bwd with a workspace)", (long long)P, (long long)n,
                 (long long)kScratchFloats);
+  // the scratch array is the current device's: a stream of another device would run the
+  // kernels there against an address that is not valid on it
+  if (stream != nullptr) {
+    int cur = -1;
+    hipDevice_t sdev = -1;
+    hipError_t e = hipGetDevice(&cur);
+    if (e != hipSuccess) return hip_fail(e, "rmsnorm_bwd_noalloc: hipGetDevice");
+    e = hipStreamGetDevice(static_cast<hipStream_t>(stream), &sdev);
+    if (e != hipSuccess) return hip_fail(e, "rmsnorm_bwd_noalloc: hipStreamGetDevice");
+    if (sdev != cur)
+      return fail(ESEP_EINVAL, "rmsnorm_bwd_noalloc: the stream is on device %d, the current "
+                  "device is %d (make the stream's device current first)", (int)sdev, cur);
+  }
   float* part = nullptr;
   const int rc = scratch_on_current_device(&part);
   if (rc != 0) return rc;

@@ -136,10 +136,11 @@ int esep_rmsnorm_bwd(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
  * Arguments are those of esep_rmsnorm_bwd without dw_partials / n_partials; dw is required.
  * Limit: esep_rmsnorm_partials(rows, n) * n <= 2^21 floats (config 4's 8192 x 1536 and config
  * 5's 65536 x 3584 fit), else ESEP_ESHAPE. The scratch array belongs to the device current on
- * the calling thread (the stream must be on that device); its address is looked up there on
- * the first call. Every call fully writes the partials it then reads, but all calls on one GPU
- * share the array: calls that can overlap on one GPU (on different streams, or from threads
- * that do not order their streams) race and must not be issued.
+ * the calling thread; its address is looked up there on the first call. A non-NULL stream on
+ * another device is rejected with ESEP_EINVAL before anything is launched. Every call fully
+ * writes the partials it then reads, but all calls on one GPU share the array: calls that can
+ * overlap on one GPU (on different streams, or from threads that do not order their streams)
+ * race and must not be issued.
  */
 int esep_rmsnorm_bwd_noalloc(const void* const* dys, int n_dy, int dy_dt, int64_t ld_dy,
                              const float* dr_out,

@@ -63,3 +63,37 @@ def test_noalloc_rejects_partials_beyond_the_scratch():
     rc = lib.esep_rmsnorm_bwd_noalloc(arr, 1, 2, 8, None, 64, 2, 8, 0, None, 64, None, None,
                                       0, None, 64, 2, 8, None, 0, 4, 8, EPS, None)
     assert rc == -1 and b"dw is required" in lib.esep_last_error()
+
+
+def test_noalloc_stream_on_the_current_device():
+    """A stream of the current device (not torch's current stream) is accepted and gives the same
+    bits as the workspace entry point on it."""
+    hip, lib = _lib()
+    x, dy, w, rstd = _inputs(1000, 1536, 9)
+    hip.rmsnorm_fwd(x, w, torch.empty_like(x), EPS, rstd=rstd)
+    dx_ref, dw_ref = torch.empty_like(x), torch.empty(1536, device=DEV)
+    hip.rmsnorm_bwd([dy], x, w, EPS, rstd=rstd, dx=dx_ref, dw=dw_ref)
+    torch.cuda.synchronize()
+    s = torch.cuda.Stream()
+    with torch.cuda.stream(s):
+        dx, dw = torch.full_like(x, float("nan")), torch.full((1536,), float("nan"), device=DEV)
+        assert _noalloc(lib, x, dy, w, rstd, dx, dw) == 0, lib.esep_last_error()
+    s.synchronize()
+    assert torch.equal(dx, dx_ref) and torch.equal(dw, dw_ref)
+
+
+@pytest.mark.skipif(torch.cuda.device_count() < 2, reason="needs a second GPU for a stream on "
+                    "another device; this pool's boxes have one")
+def test_noalloc_rejects_a_stream_of_another_device():
+    hip, lib = _lib()
+    x, dy, w, rstd = _inputs(64, 1536, 10)
+    dx, dw = torch.empty_like(x), torch.empty(1536, device=DEV)
+    other = torch.cuda.Stream(device=1)
+    arr = (ctypes.c_void_p * 5)(dy.data_ptr())
+    with torch.cuda.device(0):
+        rc = lib.esep_rmsnorm_bwd_noalloc(arr, 1, 2, 1536, None, x.data_ptr(), 2, 1536, 0,
+                                          rstd.data_ptr(), w.data_ptr(), None, None, 0, None,
+                                          dx.data_ptr(), 2, 1536, dw.data_ptr(), 0, 64, 1536, EPS,
+                                          other.cuda_stream)
+    assert rc == -1  # ESEP_EINVAL
+    assert b"device" in lib.esep_last_error()
