@@ -36,6 +36,7 @@ rmsnorm(x, weight, eps, out_dtype=None, recompute_rstd=False) -> y
 
 import math
 import threading
+import weakref
 
 import torch
 
@@ -115,26 +116,53 @@ def _rows_of(t, dtype=None):
 # instead of one per norm), then accumulates the results into .grad. The gradients are the same
 # bits either way. It is not used (each backward reduces its own partials and returns dw as
 # usual) under autograd.grad or backward(inputs=...) without the weight, with hooks on the
-# weight, for a double backward (create_graph=True), or inside a torch.distributed job (whose
-# gradient hooks expect every gradient through autograd).
+# weight, for a double backward (create_graph=True), inside a torch.distributed job (whose
+# gradient hooks expect every gradient through autograd), for a weight that is not a parameter
+# or its dtype cast (p * 0.5, a row of a stacked parameter: autograd applies their chain rule),
+# and whenever the autograd engine's entry points it relies on are missing or fail. Partials of a
+# pass that ends in an exception are dropped with the pass.
 DEFER_WEIGHT_GRAD = True
 
 _defer_lock = threading.Lock()
 _deferred = {}  # autograd graph task id -> [(weight leaf, partials, stream)]
 
+# grad_fn types of the chain _weight_f32 builds between a trainable weight and the kernel's
+# fp32 weight: a dtype cast and a contiguous copy, whose chain rule is a cast back / identity
+_CAST_NODES = ("ToCopyBackward0", "CloneBackward0")
+
 
 def _weight_leaf(w):
-    """The leaf parameter a kernel weight comes from: w itself, or the leaf behind the
-    single-input casts of _weight_f32 (None when there is no such leaf)."""
+    """The trainable leaf parameter behind the kernel weight w, when w is that leaf or comes from
+    it through the casts _weight_f32 makes (dtype cast, contiguous copy: nothing else) with the
+    same shape and device; else None. Only such a leaf can take the deferred gradient, which is
+    written into its .grad directly (cast to its dtype: the casts' own chain rule); any other
+    weight (p * 0.5, a row of a stacked parameter, a view) takes the per-call path and gets its
+    gradient through autograd."""
     if w.is_leaf:
         return w if w.requires_grad else None
-    node = w.grad_fn
-    while node is not None and type(node).__name__ != "AccumulateGrad":
+    node, hops = w.grad_fn, 0
+    while node is not None and type(node).__name__ in _CAST_NODES and hops < 2:
         nxt = [f for f, _ in node.next_functions if f is not None]
         if len(nxt) != 1:
             return None
-        node = nxt[0]
-    return getattr(node, "variable", None)
+        node, hops = nxt[0], hops + 1
+    if node is None or type(node).__name__ != "AccumulateGrad":
+        return None
+    leaf = getattr(node, "variable", None)
+    if leaf is None or leaf.shape != w.shape or leaf.device != w.device:
+        return None
+    return leaf
+
+
+def _engine():
+    """The autograd engine's entry points the deferral uses (looked up at each call), or None
+    when this torch lacks one of them: the per-call path then serves every backward."""
+    try:
+        return (torch.autograd.graph.get_gradient_edge, torch._C._will_engine_execute_node,
+                torch._C._current_graph_task_id,
+                torch.autograd.Variable._execution_engine.queue_callback)
+    except AttributeError:
+        return None
 
 
 def _can_defer(leaf):
@@ -144,30 +172,78 @@ def _can_defer(leaf):
         return False
     if torch.distributed.is_available() and torch.distributed.is_initialized():
         return False
+    eng = _engine()
+    if eng is None:
+        return False
+    get_edge, will_execute = eng[0], eng[1]
     try:
-        node = torch.autograd.graph.get_gradient_edge(leaf).node
-        return bool(torch._C._will_engine_execute_node(node))
-    except RuntimeError:
+        return bool(will_execute(get_edge(leaf).node))
+    except Exception:  # outside a backward pass, or an engine that changed: per call
         return False
 
 
-def _defer(leaf, partials):
-    """Keep one norm's partials for the end of the current backward pass."""
-    task = torch._C._current_graph_task_id()
-    stream = torch.cuda.current_stream(partials.device)
+class _PassToken:
+    """Held by the end-of-pass callback of one backward pass (graph task). The engine drops its
+    callbacks when the pass ends, normally or by an exception; the token then dies and takes the
+    pass's entries (partials included) out of _deferred if the callback never ran."""
+
+    __slots__ = ("task", "__weakref__")
+
+    def __init__(self, task):
+        self.task = task
+
+
+def _drop_task(task):
     with _defer_lock:
-        first = task not in _deferred
-        _deferred.setdefault(task, []).append((leaf, partials, stream))
+        _deferred.pop(task, None)
+
+
+def _defer(leaf, partials):
+    """Keep one norm's partials for the end of the current backward pass. Returns False (nothing
+    kept: the caller reduces them itself) when the engine's entry points are missing or fail."""
+    eng = _engine()
+    if eng is None:
+        return False
+    current_task, queue_callback = eng[2], eng[3]
+    try:
+        task = current_task()
+        stream = torch.cuda.current_stream(partials.device)
+    except Exception:
+        return False
+    with _defer_lock:
+        entries = _deferred.get(task)
+        first = entries is None
+        if first:
+            entries = _deferred[task] = []
     if first:
-        torch.autograd.Variable._execution_engine.queue_callback(lambda: _finish_deferred(task))
+        token = _PassToken(task)
+        weakref.finalize(token, _drop_task, task)
+        try:
+            queue_callback(lambda: _finish_deferred(token))
+        except Exception:
+            _drop_task(task)
+            return False
+    with _defer_lock:
+        entries.append((leaf, partials, stream))
+    return True
 
 
-def _finish_deferred(task):
+def _weight_grad_or_defer(ctx, partials):
+    """After a backward kernel wrote a deferred norm's partials: None when they were queued for
+    the end of the pass, else their stage 2 now (the per-call gradient)."""
+    if _defer(ctx.weight_leaf, partials):
+        return None
+    dw = torch.empty((partials.shape[1],), device=partials.device, dtype=torch.float32)
+    _hip.dgamma_reduce(partials, dw)
+    return dw
+
+
+def _finish_deferred(token):
     """End of a backward pass: stage 2 of every deferred norm, batched per (device, dtype, n),
     accumulated into the weights' .grad on the caller's current stream (the engine has made it
     wait for the leaf streams; the streams the partials were written on are waited for too)."""
     with _defer_lock:
-        items = _deferred.pop(task, [])
+        items = _deferred.pop(token.task, [])
     groups = {}
     for leaf, part, stream in items:
         key = (part.device, leaf.dtype, part.shape[1])
@@ -273,7 +349,7 @@ class AddRMSNorm(torch.autograd.Function):
                              slot=slots if ctx.n_special else None, xs=xs,
                              n_special=ctx.n_special, dr=dr, dx=ddelta, dw=dw, partials=partials)
             if partials is not None:
-                _defer(ctx.weight_leaf, partials)
+                dw = _weight_grad_or_defer(ctx, partials)
         elif dw is not None:
             dw.zero_()
         d_rin = dr.view(ctx.shape) if want_r else None
@@ -364,7 +440,7 @@ class RMSNorm(torch.autograd.Function):
             out = dict(dr=dx) if x2.dtype == torch.float32 else dict(dx=dx)
             _hip.rmsnorm_bwd([dy2], x2, w, ctx.eps, rstd=rstd, dw=dw, partials=partials, **out)
             if partials is not None:
-                _defer(ctx.weight_leaf, partials)
+                dw = _weight_grad_or_defer(ctx, partials)
         elif dw is not None:
             dw.zero_()
         return (dx.view(ctx.shape) if want_x else None), dw, None, None, None

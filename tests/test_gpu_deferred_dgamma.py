@@ -170,3 +170,117 @@ def test_deferred_inside_graph_capture_replays():
         graph.replay()
         torch.cuda.synchronize()
         assert torch.equal(captured, eager)
+
+
+@pytest.mark.parametrize("kind", ["scaled", "stacked_row", "exp"])
+def test_derived_weight_gets_the_chain_rule(kind):
+    """A weight computed from a parameter (p * 0.5, a row of a stacked [3, H] parameter, exp(p))
+    is not the parameter or its cast: its gradient goes through autograd per call, so .grad is the
+    same with deferral on and off, and equals the chain rule of the fp64 oracle's dw."""
+    nr = _nr()
+    g = gen(21)
+    x = randn((300, H), g, dtype=torch.bfloat16)
+    gy = randn((300, H), g, dtype=torch.bfloat16)
+    base = (1 + 0.02 * torch.randn(3, H, generator=g)) if kind == "stacked_row" else \
+        (1 + 0.02 * torch.randn(H, generator=g))
+    grads, w_eff = [], None
+    for defer in (True, False):
+        p = torch.nn.Parameter(base.clone().to(DEV))
+        w_eff = {"scaled": lambda: p * 0.5, "stacked_row": lambda: p[1],
+                 "exp": lambda: p.exp()}[kind]()
+        old = nr.DEFER_WEIGHT_GRAD
+        nr.DEFER_WEIGHT_GRAD = defer
+        try:
+            (nr.rmsnorm(x, w_eff, EPS).float() * gy.float()).sum().backward()
+        finally:
+            nr.DEFER_WEIGHT_GRAD = old
+        torch.cuda.synchronize()
+        grads.append(p.grad.clone())
+    assert torch.equal(grads[0], grads[1])
+    _, dw64 = ref.rmsnorm_bwd(np64(gy), np64(x), np64(w_eff.detach()), EPS)
+    if kind == "scaled":
+        want = 0.5 * dw64
+    elif kind == "exp":
+        want = dw64 * np64(w_eff.detach())
+    else:
+        want = np.zeros((3, H))
+        want[1] = dw64
+    assert_close(np64(grads[0]), want, 1e-4 * np.abs(want).max(), 1e-4, "grad")
+
+
+def test_pass_that_raises_drops_its_partials():
+    """A backward pass that raises after a norm deferred its partials (the failing node is
+    upstream of the norm) leaves nothing queued once the pass is gone, and the next pass gives
+    the per-call gradient."""
+    import gc
+    import time
+
+    nr = _nr()
+
+    class Boom(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, x):
+            return x.clone()
+
+        @staticmethod
+        def backward(ctx, g):
+            raise RuntimeError("planted failure upstream of the norm")
+
+    g = gen(22)
+    w = torch.nn.Parameter((1 + 0.02 * torch.randn(H, generator=g)).to(DEV))
+    x = randn((256, H), g, dtype=torch.bfloat16).requires_grad_()
+    gy = randn((256, H), g, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="planted failure"):
+        (nr.rmsnorm(Boom.apply(x), w, EPS).float() * gy.float()).sum().backward()
+    for _ in range(100):  # the engine releases the failed pass (and its callbacks) on its own
+        gc.collect()
+        if not nr._deferred:
+            break
+        time.sleep(0.01)
+    assert not nr._deferred
+    assert w.grad is None
+    (nr.rmsnorm(x, w, EPS).float() * gy.float()).sum().backward()
+    torch.cuda.synchronize()
+    assert not nr._deferred
+    wr = torch.nn.Parameter(w.detach().clone())
+    old = nr.DEFER_WEIGHT_GRAD
+    nr.DEFER_WEIGHT_GRAD = False
+    try:
+        (nr.rmsnorm(x, wr, EPS).float() * gy.float()).sum().backward()
+    finally:
+        nr.DEFER_WEIGHT_GRAD = old
+    assert torch.equal(w.grad, wr.grad)
+
+
+def test_deferral_falls_back_when_the_engine_callback_fails(monkeypatch):
+    """If queueing the end-of-pass callback fails, the norm reduces its own partials and returns
+    dw through autograd: the same bits as the per-call path."""
+    nr = _nr()
+
+    real = torch.autograd.Variable._execution_engine
+
+    class Engine:
+        """The real engine, except that it refuses end-of-pass callbacks."""
+
+        def __getattr__(self, name):
+            return getattr(real, name)
+
+        def queue_callback(self, cb):
+            raise RuntimeError("no callbacks here")
+
+    g = gen(23)
+    w = torch.nn.Parameter((1 + 0.02 * torch.randn(H, generator=g)).to(DEV))
+    x = randn((256, H), g, dtype=torch.bfloat16)
+    gy = randn((256, H), g, dtype=torch.bfloat16)
+    wr = torch.nn.Parameter(w.detach().clone())
+    old = nr.DEFER_WEIGHT_GRAD
+    nr.DEFER_WEIGHT_GRAD = False
+    try:
+        (nr.rmsnorm(x, wr, EPS).float() * gy.float()).sum().backward()
+    finally:
+        nr.DEFER_WEIGHT_GRAD = old
+    monkeypatch.setattr(torch.autograd.Variable, "_execution_engine", Engine())
+    (nr.rmsnorm(x, w, EPS).float() * gy.float()).sum().backward()
+    torch.cuda.synchronize()
+    assert not nr._deferred
+    assert torch.equal(w.grad, wr.grad)

@@ -131,3 +131,52 @@ def test_warmup_in_a_fresh_interpreter():
     r = subprocess.run([sys.executable, "-c", missing], env=env, capture_output=True, text=True,
                        timeout=300)
     assert r.returncode == 0 and "raised" in r.stdout, r.stderr[-2000:]
+
+
+def test_weight_leaf_only_through_the_casts():
+    """The deferred weight gradient is written straight into a leaf's .grad, so the leaf is taken
+    only where the kernel weight is the parameter itself or _weight_f32's cast / copy of it."""
+    from solution.body import norm_rope as nr
+
+    p = torch.nn.Parameter(torch.ones(8))
+    pb = torch.nn.Parameter(torch.ones(8, dtype=torch.bfloat16))
+    stacked = torch.nn.Parameter(torch.ones(3, 8))
+    assert nr._weight_leaf(nr._weight_f32(p, True)) is p
+    assert nr._weight_leaf(nr._weight_f32(pb, True)) is pb
+    for w in (nr._weight_f32(p * 0.5, True), nr._weight_f32(p.exp(), True),
+              nr._weight_f32(stacked[1], True), nr._weight_f32(p.view(2, 4).view(8), True),
+              nr._weight_f32(stacked.to(torch.float64)[1], True)):
+        assert nr._weight_leaf(w) is None
+    assert nr._weight_leaf(torch.ones(8)) is None  # no gradient wanted
+
+
+def _can_defer_inside_backward(nr):
+    """_can_defer for a parameter whose AccumulateGrad runs in the pass, evaluated inside a CPU
+    backward (what the norm backward sees)."""
+    leaf = torch.nn.Parameter(torch.ones(4))
+    seen = []
+
+    class Probe(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, x, w):
+            return x.clone()
+
+        @staticmethod
+        def backward(ctx, g):
+            seen.append(nr._can_defer(leaf))
+            return g, torch.zeros_like(leaf)
+
+    Probe.apply(torch.ones(4, requires_grad=True), leaf).sum().backward()
+    return seen[0]
+
+
+def test_can_defer_without_engine_internals(monkeypatch):
+    """The deferral rests on private autograd entry points: with one of them gone (a torch
+    without it) _can_defer answers False instead of raising, and _defer declines."""
+    from solution.body import norm_rope as nr
+
+    assert _can_defer_inside_backward(nr) is True
+    monkeypatch.delattr(torch._C, "_will_engine_execute_node")
+    assert _can_defer_inside_backward(nr) is False
+    assert nr._defer(None, torch.empty(1, 8)) is False
+    assert not nr._deferred
