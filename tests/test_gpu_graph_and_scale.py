@@ -7,9 +7,10 @@ memset and allocates nothing, so replays are self-contained).
 
 Config 5 (T = 65536 packed tokens, H = 3584, 28 / 4 heads, varlen U[128, 4096]): too large for
 the fp64 oracle as a whole, so it is checked through properties that do not depend on size:
-sampled rows against the oracle, the weight gradient as the sum of its halves (linearity over
-rows), cu_seqlens positions equal to explicit positions bitwise, and RoPE forward-then-backward
-returning the input."""
+sampled rows against the oracle, the weight gradient on sampled columns against its closed form
+summed over all rows in fp64 and as the sum of its halves (linearity over rows), cu_seqlens
+positions equal to explicit positions bitwise, and RoPE forward-then-backward returning the
+input."""
 
 import numpy as np
 import pytest
@@ -89,6 +90,21 @@ def _config5():
     return bench.CFG5, bench.config5_lengths(bench.CFG5)
 
 
+def _dw_columns_fp64(x, dy, w, cols, chunk=8192):
+    """The weight gradient's closed form on columns `cols`, over every row, in fp64 on the CPU:
+    dw_j = sum_t dy_tj * x_tj * rstd_t with each row's rstd from the oracle's forward on the
+    whole row (chunks of rows), and the column sums from the oracle's backward given that rstd."""
+    T = x.shape[0]
+    wn = np64(w)
+    out = np.zeros(len(cols))
+    for t0 in range(0, T, chunk):
+        xc = np64(x[t0:t0 + chunk])
+        _, rstd = ref.rmsnorm_fwd(xc, wn, EPS)
+        _, dw = ref.rmsnorm_bwd(np64(dy[t0:t0 + chunk, cols]), xc[:, cols], wn[cols], EPS, rstd=rstd)
+        out += dw
+    return out
+
+
 def test_config5_rmsnorm_full_size():
     from solution.body import norm_rope
 
@@ -117,6 +133,35 @@ def test_config5_rmsnorm_full_size():
     # and the same call twice gives the same bits
     dw2 = torch.autograd.grad(norm_rope.rmsnorm(x, w, EPS), [w], dy)[0]
     assert torch.equal(dw, dw2)
+    # 64 sampled columns against the closed form summed over all 65536 rows in fp64
+    cols = sorted(set([0, H - 1] + torch.randint(0, H, (62,), generator=gen(3)).tolist()))
+    want = _dw_columns_fp64(x.detach(), dy, w.detach(), cols)
+    assert_close(np64(dw)[cols], want, 1e-5 * np.abs(want).max(), 1e-5, "dw columns vs fp64")
+
+
+def test_config5_bench_norm_backward_weight_gradient():
+    """The bench's own config-5 launch (bench.Stress: the C ABI with a workspace, 512 partial
+    rows, the wide kernel) against the weight gradient's closed form in fp64 on 64 columns over
+    all rows, and its dx on sampled rows against the oracle."""
+    import bench
+
+    cfg = bench.CFG5
+    st = bench.Stress(cfg, torch.device(DEV))
+    from solution.body import _hip
+
+    assert st.ws.shape[0] == _hip.rmsnorm_partials(cfg["T"], cfg["H"]) == 512
+    st.norm_fwd()
+    st.norm_bwd()
+    torch.cuda.synchronize()
+    T, H = cfg["T"], cfg["H"]
+    cols = sorted(set([0, H - 1] + torch.randint(0, H, (62,), generator=gen(4)).tolist()))
+    want = _dw_columns_fp64(st.x, st.dy, st.w, cols)
+    assert_close(np64(st.dw)[cols], want, 1e-5 * np.abs(want).max(), 1e-5, "bench dw vs fp64")
+    rows = torch.randint(0, T, (32,), generator=gen(6)).tolist() + [0, T - 1]
+    dx64, _ = ref.rmsnorm_bwd(np64(st.dy[rows]), np64(st.x[rows]), np64(st.w), EPS)
+    assert_close(np64(st.dx[rows]), ref.round_to(dx64, "bf16"), 2e-3, 1e-2, "bench dx")
+    del st
+    torch.cuda.empty_cache()
 
 
 def test_config5_rope_full_size():
