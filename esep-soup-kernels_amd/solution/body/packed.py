@@ -16,18 +16,20 @@ Per decoder layer, each piece has a guard and an HF / torch fallback (warned onc
               post-attention norm: gate and up) so their gradients are summed in the norm
               backward. A trainable norm weight stays on the kernel (its gradient comes from the
               kernel's two-stage reduction); the reference hands it to HF (its packed.py:129).
-  q/k/v       the model's projections; a peft-style LoRA projection (base_layer + lora_A /
+  q/k/v/o     the model's projections; a peft-style LoRA projection (base_layer + lora_A /
               lora_B / lora_dropout / scaling, one active adapter) runs its base layer directly
               and its LoRA term on lora.py: v's added into the base output, q's passed to the
-              RoPE kernel as q_delta (reference packed.py:240-352).
+              RoPE kernel as q_delta (reference packed.py:240-352). NF4 base layers
+              (bitsandbytes' Linear4bit interface, solution.nf4) run through nf4.linear4bit on
+              the HIP dequant, and q/k/v on NF4 bases as one nf4.linear4bit_multi call (one
+              dequant launch and one GEMM) on the input norm's output (reference :184-352).
   RoPE        norm_rope.rope on the packed positions with the model's inv_freq.
   attention   attention.varlen_attention over all rows in one launch per direction; else a
               per-row SDPA loop (reference packed.py:404-436).
-  MLP         frozen plain projections: _RecomputeMLP (no [T, intermediate] tensor saved);
+  MLP         frozen plain or NF4 projections: _RecomputeMLP (no [T, intermediate] tensor
+              saved; NF4 weights dequantized on the HIP kernel, gate and up in one launch);
               otherwise the projections with the HIP SwiGLU, gate and up fed from their own
               copies of the norm output.
-The NF4 / bitsandbytes projection routes of the reference (its packed.py:184-238, :440-561)
-need bitsandbytes, which this build does not have; those projections run as modules.
 """
 
 import contextlib
@@ -176,17 +178,35 @@ def _add_norm(norm, residual, delta, final=False, with_eps=False, n_out=1, save_
 # ----------------------------------------------------------------------------------------
 # projections and their LoRA terms
 # ----------------------------------------------------------------------------------------
+def _nf4():
+    from .. import nf4
+
+    return nf4
+
+
+def _fp16_under_autocast(x):
+    return (x.dtype == torch.float16 and x.is_cuda and torch.is_autocast_enabled("cuda")
+            and torch.get_autocast_dtype("cuda") == torch.float16)
+
+
 def _lora_route(module, x):
     """How a projection runs on the packed 16-bit x [1, T, in]:
-      (base layer, None)              a LoRA wrapper with no adapter active: its base alone;
+      (base layer, None)              the base layer alone: an NF4 Linear4bit itself, or a LoRA
+                                      wrapper with no adapter active;
       (base layer, (A, B, p, scale))  a LoRA wrapper this path runs (lora.lora_params);
       None                            anything else, or a guard failed: module(x).
     A LoRA wrapper is any module with peft's LoRA layer attributes (base_layer, lora_A, lora_B,
-    lora_dropout, scaling, active_adapters) whose base is a plain nn.Linear. The path needs the
-    kernels on, a device x in fp16 / bf16 under autocast to that dtype (peft computes the term
-    in the autocast dtype then), and no hooks (reference packed.py:240-290)."""
+    lora_dropout, scaling, active_adapters) whose base is a plain nn.Linear or an NF4 Linear4bit
+    (nf4.is_linear4bit). The path needs the kernels on, a device x in fp16 / bf16 under autocast
+    to that dtype (peft computes the term in the autocast dtype then; fp16 for an NF4 base, whose
+    linear4bit computes in fp16), and no hooks (reference packed.py:240-290)."""
     if not (USE_KERNELS and USE_LORA_KERNELS):
         return None
+    nf4 = _nf4()
+    if nf4.is_linear4bit(module):
+        if not _fp16_under_autocast(x) or _has_hooks(module):
+            return _fallback("NF4 path", f"x {x.dtype}, no fp16 autocast, or hooks")
+        return module, None
     base = getattr(module, "base_layer", None)
     if base is None or not hasattr(module, "lora_A"):
         return None
@@ -194,8 +214,11 @@ def _lora_route(module, x):
         return _fallback("LoRA path", f"x {x.dtype} {x.device}")
     if not torch.is_autocast_enabled("cuda") or torch.get_autocast_dtype("cuda") != x.dtype:
         return _fallback("LoRA path", f"no autocast to {x.dtype}")
-    if _has_hooks(module) or type(base) is not torch.nn.Linear or _has_hooks(base):
+    nf4_base = nf4.is_linear4bit(base)
+    if _has_hooks(module) or not (type(base) is torch.nn.Linear or nf4_base) or _has_hooks(base):
         return _fallback("LoRA path", f"{type(module).__name__} / {type(base).__name__} or hooks")
+    if nf4_base and x.dtype != torch.float16:
+        return _fallback("LoRA path", f"NF4 base under {x.dtype} autocast")
     if getattr(module, "disable_adapters", False) or getattr(module, "merged", False):
         return _fallback("LoRA path", "adapters disabled or merged")
     if not any(name in module.lora_A for name in getattr(module, "active_adapters", ())):
@@ -208,17 +231,26 @@ def _lora_route(module, x):
     return base, params
 
 
+def _base(base, x2):
+    """The base projection on the 2-D x (a fresh output): an NF4 Linear4bit through
+    nf4.linear4bit (its fp16 output), anything else through its own forward."""
+    nf4 = _nf4()
+    if nf4.is_linear4bit(base):
+        return nf4.linear4bit(x2, base, keep_fp16=True)
+    return base(x2)
+
+
 def _project(module, x, x_lora=None):
-    """module(x) for x [1, T, in] -> [1, T, out]. A routed LoRA projection runs its base on the
-    2-D x (a fresh output: F.linear with a bias on a 3-D input can return a view) and adds its
-    LoRA term into that output; x_lora is the LoRA term's own copy of the norm output (same
-    values), so the two input gradients reach the norm backward apart."""
+    """module(x) for x [1, T, in] -> [1, T, out]. A routed projection runs its base on the 2-D x
+    (a fresh output: F.linear with a bias on a 3-D input can return a view) and adds its LoRA
+    term into that output; x_lora is the LoRA term's own copy of the norm output (same values),
+    so the two input gradients reach the norm backward apart."""
     route = _lora_route(module, x)
     if route is None:
         return module(x)
     base, params = route
     x2 = x.reshape(-1, x.shape[-1])
-    out = base(x2)
+    out = _base(base, x2)
     if params is not None:
         from .lora import LoRAFunction
 
@@ -238,10 +270,39 @@ def _project_q(module, x, x_lora=None):
     from .lora import LoRADeltaFunction
 
     x2 = x.reshape(-1, x.shape[-1])
-    q = base(x2)
+    q = _base(base, x2)
     xl = x2 if x_lora is None else x_lora.reshape(-1, x_lora.shape[-1])
     term = LoRADeltaFunction.apply(xl, *params)
     return q.view(1, x2.shape[0], -1), term.view(1, x2.shape[0], -1)
+
+
+def _qkv(attn, x_q, x_ql, x_vl):
+    """(q, q term, k, v) as _project_q / _project give them, with the three base projections as
+    ONE nf4.linear4bit_multi call on x_q (one dequant launch into W_cat, one GEMM; backward one
+    re-dequant and one dX GEMM) when q, k and v all take this path onto NF4 bases, k without a
+    LoRA term of its own; else None (the separate calls run). q, k, v are column views of the
+    one output; v's LoRA term is added out of place (v is a view). The norm backward then gets
+    one base gradient (through x_q) beside the q and v LoRA gradients (x_ql, x_vl); the k and v
+    base copies of the norm output get none (reference packed.py:321-352)."""
+    routes = [_lora_route(m, x_q) for m in (attn.q_proj, attn.k_proj, attn.v_proj)]
+    if any(r is None for r in routes) or routes[1][1] is not None:
+        return None
+    nf4 = _nf4()
+    bases = [r[0] for r in routes]
+    if not all(nf4.is_linear4bit(b) for b in bases):
+        return None
+    from .lora import LoRADeltaFunction, LoRAFunction
+
+    x2 = x_q.reshape(-1, x_q.shape[-1])
+    n_tok = x2.shape[0]
+    q, k, v = nf4.linear4bit_multi(x2, bases)
+    q_term = None
+    if routes[0][1] is not None:
+        q_term = LoRADeltaFunction.apply(x_ql.reshape(-1, x_ql.shape[-1]), *routes[0][1])
+        q_term = q_term.view(1, n_tok, -1)
+    if routes[2][1] is not None:
+        v = LoRAFunction.apply(x_vl.reshape(-1, x_vl.shape[-1]), v, *routes[2][1])
+    return q.view(1, n_tok, -1), q_term, k.view(1, n_tok, -1), v.view(1, n_tok, -1)
 
 
 # ----------------------------------------------------------------------------------------
@@ -350,39 +411,53 @@ def _plain_silu_mlp(mlp, x):
 
 def _mlp_layers(mlp, x):
     """(gate, up, down) when mlp(x) can run as _RecomputeMLP, else None (reference
-    packed.py:493-524, where the projections are frozen NF4): the kernels and RECOMPUTE_MLP on,
-    grad mode on, a plain silu Qwen2MLP whose three projections are bias-free nn.Linear without
-    hooks, nothing in it trainable, and a 16-bit device x that the projections compute in
-    (autocast to x's dtype, or weights of x's dtype)."""
+    packed.py:493-524): the kernels and RECOMPUTE_MLP on, grad mode on, a plain silu Qwen2MLP
+    without hooks whose three projections are all frozen NF4 Linear4bit (nf4.is_linear4bit)
+    without bias or hooks, with a fp16 device x under fp16 autocast (linear4bit computes in
+    fp16), or all bias-free nn.Linear without hooks with a 16-bit device x that they compute in
+    (autocast to x's dtype, or weights of x's dtype); nothing in the MLP trainable."""
     if not (USE_KERNELS and RECOMPUTE_MLP) or not torch.is_grad_enabled():
         return None
     piece = "recompute MLP"
     if x.dtype not in (torch.float16, torch.bfloat16) or not _plain_silu_mlp(mlp, x):
         return _fallback(piece, f"x {x.dtype}, {type(mlp).__name__}, hooks or activation")
     projections = (mlp.gate_proj, mlp.up_proj, mlp.down_proj)
+    if any(prm.requires_grad for prm in mlp.parameters()):
+        return _fallback(piece, "trainable parameter in the MLP")
+    nf4 = _nf4()
+    if all(nf4.is_linear4bit(lin) for lin in projections):
+        if not _fp16_under_autocast(x):
+            return _fallback(piece, f"NF4 projections with x {x.dtype} / no fp16 autocast")
+        if any(_has_hooks(lin) or lin.bias is not None for lin in projections):
+            return _fallback(piece, "NF4 projection with a bias or hooks")
+        return projections
     autocast_to_x = (torch.is_autocast_enabled("cuda")
                      and torch.get_autocast_dtype("cuda") == x.dtype)
     for lin in projections:
         if type(lin) is not torch.nn.Linear or _has_hooks(lin) or lin.bias is not None:
-            return _fallback(piece, "projection not a plain bias-free nn.Linear")
+            return _fallback(piece, "projections not all bias-free nn.Linear or NF4 Linear4bit")
         if not autocast_to_x and lin.weight.dtype != x.dtype:
             return _fallback(piece, f"weights {lin.weight.dtype} without autocast to {x.dtype}")
-    if any(prm.requires_grad for prm in mlp.parameters()):
-        return _fallback(piece, "trainable parameter in the MLP")
     return projections
 
 
 class _RecomputeMLP(torch.autograd.Function):
     """down(silu(gate(x)) * up(x)) for frozen projections without saving any [T, intermediate]
-    tensor (the reference's activation-memory trade, packed.py:562-643, for its frozen NF4
-    projections; here frozen 16-bit nn.Linear, a LoRA run on an unquantized base).
+    tensor (the reference's activation-memory trade, packed.py:562-643): frozen NF4 Linear4bit
+    projections as in the reference, or frozen 16-bit nn.Linear (a LoRA run on an unquantized
+    base).
 
     apply(x_gate, x_up, r, w_norm, eps, gate, up, down). Saved: x itself, or (when the norm
     that produced x did not keep its output) the norm's fp32 input r and weight, x then being
     recomputed bit-exactly by the same norm kernel in backward. Forward: g, u from the two
-    projections, h = silu(g) * u on the HIP kernel (into g), out = h down^T. Backward: dh =
-    dout down, g and u recomputed, (dg, du) by the HIP kernel in place, dx_gate = dg gate and
-    dx_up = du up, returned for the two fan-out copies (the norm backward sums them)."""
+    projections (NF4: nf4.linear4bit, dequant on the HIP kernel + fp16 GEMM), h = silu(g) * u on
+    the HIP kernel (into g), out from the down projection. Backward: dh = dout W_down, g and u
+    recomputed, (dg, du) by the HIP kernel in place. NF4: W_down from one dequant launch, W_gate
+    and W_up from one esep_nf4_dequant_multi launch (row blocks bit-exact with the forward's
+    dequants, so g and u recompute bit-exactly), and dx = dg W_gate + du W_up formed as mm +
+    addmm into one buffer, returned as x_gate's gradient (x_up gets none). nn.Linear: dx_gate =
+    dg gate and dx_up = du up, returned for the two fan-out copies (the norm backward sums
+    them)."""
 
     @staticmethod
     @torch.amp.custom_fwd(device_type="cuda")
@@ -391,10 +466,18 @@ class _RecomputeMLP(torch.autograd.Function):
 
         shape = x.shape
         x2 = x.reshape(-1, shape[-1])
-        h = F.linear(x2, gate.weight).contiguous()
-        u = F.linear(x2, up.weight).contiguous()
-        _hip.swiglu_fwd(h, u, h)
-        out = F.linear(h, down.weight)
+        nf4 = _nf4()
+        ctx.nf4 = nf4.is_linear4bit(gate)
+        if ctx.nf4:
+            h = nf4.linear4bit(x2, gate, keep_fp16=True).contiguous()
+            u = nf4.linear4bit(x2, up, keep_fp16=True).contiguous()
+            _hip.swiglu_fwd(h, u, h)
+            out = nf4.linear4bit(h, down, keep_fp16=True)
+        else:
+            h = F.linear(x2, gate.weight).contiguous()
+            u = F.linear(x2, up.weight).contiguous()
+            _hip.swiglu_fwd(h, u, h)
+            out = F.linear(h, down.weight)
         del h, u
         if r is None:
             ctx.save_for_backward(x2)
@@ -417,7 +500,24 @@ class _RecomputeMLP(torch.autograd.Function):
             x2 = rmsnorm_recompute(r.reshape(-1, r.shape[-1]), w_norm, ctx.eps, ctx.x_dtype)
         else:
             (x2,) = ctx.saved_tensors
-        dh = torch.matmul(dout.reshape(-1, dout.shape[-1]), down.weight)
+        dout2 = dout.reshape(-1, dout.shape[-1])
+        if ctx.nf4:
+            nf4 = _nf4()
+            w = nf4.dequantize_nf4(down.weight, down.weight.quant_state)
+            dh = torch.matmul(dout2.to(w.dtype), w)
+            del w
+            w_gu = nf4.dequant_multi([gate, up])
+            n_gate = gate.weight.quant_state.shape[0]
+            w_gate, w_up = w_gu[:n_gate], w_gu[n_gate:]
+            g = F.linear(x2, w_gate).contiguous()
+            u = F.linear(x2, w_up).contiguous()
+            del x2
+            _hip.swiglu_bwd(dh.contiguous(), g, u, g, u)  # dg into g, du into u
+            del dh
+            dx = torch.mm(g, w_gate)
+            dx.addmm_(u, w_up)
+            return dx.view(ctx.shape), None, None, None, None, None, None, None
+        dh = torch.matmul(dout2, down.weight)
         g = F.linear(x2, gate.weight).contiguous()
         u = F.linear(x2, up.weight).contiguous()
         del x2
@@ -460,16 +560,21 @@ def _layer(layer, residual, delta, rope_in, lens):
     """One Qwen2DecoderLayer on the packed tokens (reference packed.py:696-724). Returns
     (residual, delta): the layer's output is residual + delta, the add left to the next norm.
     The input norm's output goes to five consumers, each with its own copy: q, k and v
-    projections and the q and v LoRA terms (a copy nothing consumes gets no gradient)."""
+    projections and the q and v LoRA terms (a copy nothing consumes gets no gradient; with the
+    fused NF4 q/k/v call, the k and v base copies)."""
     attn = layer.self_attn
     residual, (x_q, x_ql, x_k, x_v, x_vl) = _add_norm(layer.input_layernorm, residual, delta,
                                                       n_out=5, save_output=NORM_SAVE_OUTPUT)
     n_tok, head_dim = x_q.shape[1], attn.head_dim
-    q, q_term = _project_q(attn.q_proj, x_q, x_ql)
-    k = _project(attn.k_proj, x_k)
-    v = _project(attn.v_proj, x_v, x_vl)
+    fused = _qkv(attn, x_q, x_ql, x_vl)
+    if fused is not None:
+        q, q_term, k, v = fused
+    else:
+        q, q_term = _project_q(attn.q_proj, x_q, x_ql)
+        k = _project(attn.k_proj, x_k)
+        v = _project(attn.v_proj, x_v, x_vl)
     q, k = _rope(q.view(1, n_tok, -1, head_dim), k.view(1, n_tok, -1, head_dim), rope_in, q_term)
-    o = attn.o_proj(_attention(attn, q, k, v.view(1, n_tok, -1, head_dim), lens))
+    o = _project(attn.o_proj, _attention(attn, q, k, v.view(1, n_tok, -1, head_dim), lens))
     post = layer.post_attention_layernorm
     residual, xs, eps = _add_norm(post, residual, o, with_eps=True, n_out=2,
                                   save_output=NORM_SAVE_OUTPUT)

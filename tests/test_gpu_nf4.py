@@ -84,7 +84,7 @@ def test_dequantize_nf4_api_multi_and_linear():
     packed, qs, _ = states[0]
     x = torch.randn(4, 7, 128, device=DEV, dtype=torch.float16, requires_grad=True)
     bias = torch.randn(96, device=DEV, dtype=torch.float16)
-    y = nf4.nf4_linear(x, packed, qs, bias)
+    y = nf4.nf4_linear(x, packed, bias, qs)
     dy = torch.randn_like(y)
     (dx,) = torch.autograd.grad(y, [x], dy)
     w16 = nf4.dequantize_nf4(packed, qs)
