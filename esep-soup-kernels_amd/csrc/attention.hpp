@@ -155,14 +155,6 @@ __device__ __forceinline__ void lds_dma_dword(const void* g, const void* lds) {
   asm volatile("global_load_lds_dword %0, off" ::"v"(g), "{m0}"(m) : "memory");
 }
 
-// The same with a wave-uniform base address in SGPRs and the lane's byte offset in a VGPR
-// (lane l reads the dword at base + voff): a row's address is then a scalar add, not a 64-bit
-// multiply per lane.
-__device__ __forceinline__ void lds_dma_dword_s(const void* base, uint32_t voff, const void* lds) {
-  const uint32_t m = __builtin_amdgcn_readfirstlane((uint32_t)(uintptr_t)lds);
-  asm volatile("global_load_lds_dword %0, %1" ::"v"(voff), "s"(base), "{m0}"(m) : "memory");
-}
-
 // s_waitcnt vmcnt(0) (expcnt, lgkmcnt left at their maxima): through the builtin, so that the
 // compiler's own wait tracking sees it too.
 constexpr int kWaitVm0 = 0x0F70;

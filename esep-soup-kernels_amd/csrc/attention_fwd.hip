@@ -161,105 +161,6 @@ __global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd(const AttnArgs a) 
     a.lse[(int64_t)h * a.T + qi] = (m + log2f(l)) * 0.69314718055994531f;
 }
 
-// D = 128 forward with the K / V tiles moved by LDS DMA (lds_dma_dword: one 256-byte token row
-// per instruction, straight into LDS, no registers) in tiles of 32 keys through a ring of two
-// buffers: tile t + 1 is in flight while tile t is consumed, and one barrier per tile both
-// publishes tile t and certifies that tile t - 1 is consumed, freeing its buffer. Rows keep the
-// padded pitch, so the operand reads stay conflict-free; rows past kend repeat row kend - 1
-// (finite data; every such key is masked, so it contributes p = 0). 39 KiB of LDS per block:
-// 3 blocks per CU, as the registers allow. Measured at config 5 against the register-staged
-// kernel (64-key tiles, two barriers per tile): 2.13 -> 2.01 ms; 64-key tiles in the ring
-// (2 blocks per CU) 2.79 ms, a ring of three 32-key tiles at a 68-dword pitch 2.23 ms.
-template <typename T>
-__global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd_dma(const AttnArgs a) {
-  constexpr int D = 128;
-  constexpr int BN = 32;
-  using V8 = typename Mfma<T>::v8;
-  constexpr int KP = D + kRowPad;
-  __shared__ __align__(16) T kv[2][2][BN * KP];  // [buffer][K, V][row-major tile]
-
-  const int seq = blockIdx.z, h = blockIdx.y;
-  int start, end;
-  seq_bounds(a.cu, seq, a.T, &start, &end);
-  const int ntiles_q = (end - start + kAttnBM - 1) / kAttnBM;
-  if ((int)blockIdx.x >= ntiles_q) return;
-  const int q0 = start + (ntiles_q - 1 - (int)blockIdx.x) * kAttnBM;  // heaviest tiles first
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int lq = lane & 31, hi = lane >> 5;
-  const int kvh = h / (a.HQ / a.HK);
-  const int qw0 = q0 + 32 * w;
-  const int qi = qw0 + lq;
-  const bool wave_live = qw0 < end;
-  const int wq_last = qw0 + 31 < end ? qw0 + 31 : end - 1;
-
-  V8 qb[D / 16];
-  {
-    const T* qrow = static_cast<const T*>(a.q) + (int64_t)qi * a.q_rs + (int64_t)h * D + 8 * hi;
-#pragma unroll
-    for (int c = 0; c < D / 16; ++c)
-      qb[c] = qi < end ? ld16<V8>(qrow + 16 * c) : V8{};
-  }
-
-  f32x16 oacc[D / 32];
-#pragma unroll
-  for (int md = 0; md < D / 32; ++md) oacc[md] = f32x16{};
-  float m = -INFINITY, l = 0.f;
-  const int kend = end < q0 + kAttnBM ? end : q0 + kAttnBM;
-  const T* kbase = static_cast<const T*>(a.k) + (int64_t)kvh * D;
-  const T* vbase = static_cast<const T*>(a.v) + (int64_t)kvh * D;
-  const int ntiles = (kend - start + BN - 1) / BN;
-
-  // wavefront w moves rows w, w + 4, ... of the tile's K and V. A whole tile (the common case)
-  // walks the rows with scalar adds from the tile's row-w address; the last, partial tile
-  // clamps each row to kend - 1.
-  const int64_t k_step = 4 * a.k_rs, v_step = 4 * a.v_rs;  // elements between a wave's rows
-  const uint32_t voff = 4u * (uint32_t)lane;
-  auto issue = [&](T* kd, T* vd, int kt) {
-    if (kt + BN <= kend) {
-      const T* kr = kbase + (int64_t)(kt + w) * a.k_rs;
-      const T* vr = vbase + (int64_t)(kt + w) * a.v_rs;
-#pragma unroll
-      for (int jj = 0; jj < BN / 4; ++jj) {
-        const int j = 4 * jj + w;
-        lds_dma_dword_s(kr, voff, kd + j * KP);
-        lds_dma_dword_s(vr, voff, vd + j * KP);
-        kr += k_step;
-        vr += v_step;
-      }
-      return;
-    }
-#pragma unroll
-    for (int jj = 0; jj < BN / 4; ++jj) {
-      const int j = 4 * jj + w;
-      const int r = kt + j < kend ? kt + j : kend - 1;
-      lds_dma_dword(reinterpret_cast<const uint32_t*>(kbase + (int64_t)r * a.k_rs) + lane, kd + j * KP);
-      lds_dma_dword(reinterpret_cast<const uint32_t*>(vbase + (int64_t)r * a.v_rs) + lane, vd + j * KP);
-    }
-  };
-
-  auto consume = [&](const T* ks, const T* vs, int kt) {
-    if (!wave_live || kt > wq_last) return;  // every key of the tile is after this wave's queries
-    fwd_half<T, D, KP>(ks, vs, 0, kt, qw0, qi, lane, a.scale_log2, qb, oacc, m, l);
-  };
-
-  if (ntiles > 0) issue(kv[0][0], kv[0][1], start);
-  for (int t = 0; t < ntiles; ++t) {
-    // this wavefront's DMA of tile t has landed; the barrier publishes every wavefront's rows
-    // and certifies that tile t - 1, in the other buffer, is consumed
-    __builtin_amdgcn_s_waitcnt(kWaitVm0);
-    __syncthreads();
-    if (t + 1 < ntiles) issue(kv[(t + 1) & 1][0], kv[(t + 1) & 1][1], start + (t + 1) * BN);
-    consume(kv[t & 1][0], kv[t & 1][1], start + t * BN);
-  }
-
-  if (!wave_live || qi >= end) return;
-  store_rows_t<T, D>(static_cast<T*>(a.o) + (int64_t)qi * a.o_rs + (int64_t)h * D, oacc, hi,
-                     l > 0.f ? 1.f / l : 0.f);
-  if (hi == 0 && a.lse != nullptr)
-    a.lse[(int64_t)h * a.T + qi] = (m + log2f(l)) * 0.69314718055994531f;
-}
-
 // D = 128 forward on swizzled, unpadded LDS tiles (the layout, its DMA and its readers are in
 // attention.hpp: swz, SwzFill, swz_row_base, SwzTr).
 //
@@ -343,9 +244,10 @@ __device__ __forceinline__ void fwd_tile_swz(const char* ks, const char* vs, int
   __builtin_amdgcn_s_setprio(0);
 }
 
-// The D = 128 forward kernel: blocks, queries and the online softmax as k_attn_fwd_dma; the
-// 32-key K / V tiles go through a ring of NBUF swizzled buffers (tile t + NBUF - 1 in flight
-// while tile t is consumed).
+// The D = 128 forward kernel: blocks of 4 wavefronts own 128 queries of one (sequence, query
+// head) with the online softmax in registers; the 32-key K / V tiles go through a ring of NBUF
+// swizzled LDS buffers filled by LDS DMA (tile t + NBUF - 1 in flight while tile t is consumed,
+// one barrier per tile publishing it and freeing the buffer consumed before).
 template <typename T, int NBUF>
 __global__ __launch_bounds__(kAttnThreads, 3) void k_attn_fwd_swz(const AttnArgs a, int qtiles,
                                                                   int order) {

@@ -280,3 +280,51 @@ def test_attn_config4_shape():
         err = np.abs(g64 - w64)
         assert np.all(err <= 1e-2 * np.abs(w64).max() + 1e-2 * np.abs(w64) + 1e-5), \
             (name, float(err.max()), float(np.abs(w64).max()))
+
+
+@pytest.mark.parametrize("D", [128, 64])
+def test_attn_strided_fused_qkv(D):
+    """q, k and v as column slices of one fused [T, (HQ + 2 HK) * D] bf16 projection output (token
+    stride (HQ + 2 HK) * D, not HQ * D), and dq, dk, dv written into column slices of one fused
+    gradient buffer, with ragged lengths so partial last tiles occur: the LDS-DMA fills address
+    rows with the token stride. Output and gradients against float32 SDPA on the same values
+    (1e-2 of the largest magnitude plus 1e-2 relative), and bitwise the dense layout's results."""
+    from solution.body import _hip
+
+    lengths, HQ, HK = [37, 300, 1, 129, 64], 12, 2
+    T, W = sum(lengths), (HQ + 2 * HK) * D
+    g = gen(500 + D)
+    fused = torch.randn(T, W, generator=g).to(torch.bfloat16).to(DEV)
+    q = fused[:, :HQ * D].view(T, HQ, D)
+    k = fused[:, HQ * D:(HQ + HK) * D].view(T, HK, D)
+    v = fused[:, (HQ + HK) * D:].view(T, HK, D)
+    assert q.stride(0) == W and not q.is_contiguous()
+    cu = torch.tensor(ref.cu_from_lengths(lengths), dtype=torch.int32, device=DEV)
+    do = torch.randn(T, HQ, D, generator=gen(600 + D)).to(torch.bfloat16).to(DEV)
+    scale = D ** -0.5
+    o = torch.full((T, HQ, D), float("nan"), device=DEV, dtype=torch.bfloat16)
+    lse = torch.empty((HQ, T), device=DEV)
+    _hip.attn_fwd(q, k, v, o, cu, max(lengths), scale, lse=lse)
+    gfused = torch.full((T, W), float("nan"), device=DEV, dtype=torch.bfloat16)
+    dq = gfused[:, :HQ * D].view(T, HQ, D)
+    dk = gfused[:, HQ * D:(HQ + HK) * D].view(T, HK, D)
+    dv = gfused[:, (HQ + HK) * D:].view(T, HK, D)
+    _hip.attn_bwd(q, k, v, o, do, lse, dq, dk, dv, cu, max(lengths), scale)
+    q32, k32, v32, do32 = (t.float().contiguous() for t in (q, k, v, do))
+    want_o = _torch_sdpa(q32, k32, v32, lengths, scale)
+    want = _torch_grads(q32, k32, v32, do32, lengths, scale)
+    for name, got, w in (("o", o, want_o), ("dq", dq, want[0]), ("dk", dk, want[1]),
+                         ("dv", dv, want[2])):
+        g64, w64 = np64(got), np64(w)
+        err = np.abs(g64 - w64)
+        assert np.all(err <= 1e-2 * np.abs(w64).max() + 1e-2 * np.abs(w64) + 1e-5), \
+            (name, float(err.max()), float(np.abs(w64).max()))
+    # the dense layout gives the same bits
+    qd, kd, vd = (t.contiguous() for t in (q, k, v))
+    od = torch.empty_like(qd)
+    lsed = torch.empty_like(lse)
+    _hip.attn_fwd(qd, kd, vd, od, cu, max(lengths), scale, lse=lsed)
+    dqd, dkd, dvd = (torch.empty_like(t) for t in (qd, kd, vd))
+    _hip.attn_bwd(qd, kd, vd, od, do, lsed, dqd, dkd, dvd, cu, max(lengths), scale)
+    assert torch.equal(od, o) and torch.equal(lsed, lse)
+    assert torch.equal(dqd, dq) and torch.equal(dkd, dk) and torch.equal(dvd, dv)
