@@ -1069,6 +1069,21 @@ def _cpu_model():
     return "unknown"
 
 
+# The GPU box gives the job of its one GPU a share of 16 host cores (OMP_NUM_THREADS=16 there),
+# whatever os.sched_getaffinity reports; the CPU legs use at most that many threads.
+CPU_SHARE = 16
+
+
+def _cpu_threads():
+    return max(1, min(len(os.sched_getaffinity(0)), CPU_SHARE))
+
+
+def _cpu_threads_note():
+    return (f"{_cpu_threads()} threads: os.sched_getaffinity reports "
+            f"{len(os.sched_getaffinity(0))} cores, capped at the box's {CPU_SHARE}-core share "
+            f"for one GPU's job")
+
+
 def _cpu_time(fn, budget_s, min_reps=5):
     """Median wall time of fn() over at least min_reps runs (after one warm-up), stopping at
     budget_s or 20 runs."""
@@ -1090,7 +1105,7 @@ def cpu_configs(cfg5, budget_s=2.0):
 
     from oracle import hf_eager
 
-    threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+    threads = _cpu_threads()
     torch.set_num_threads(threads)
     g = torch.Generator().manual_seed(0)
     eps, theta, D = 1e-6, 1e6, 128
@@ -1156,7 +1171,7 @@ def cpu_baseline(cfg, budget_s=12.0, batch=2):
 
     from oracle import hf_eager
 
-    threads = max(1, min(len(os.sched_getaffinity(0)), 16))
+    threads = _cpu_threads()
     torch.set_num_threads(threads)
     model = _cpu_model()
     S, H, HQ, HK, D, eps = (cfg[k] for k in ("S", "H", "HQ", "HK", "D", "eps"))
@@ -1183,7 +1198,7 @@ def cpu_baseline(cfg, budget_s=12.0, batch=2):
     layer_bytes = 2 * (norm_fwd_bytes(T, H, e, True) + norm_bwd_bytes(T, H, e, True)) + \
         2 * rope_bytes(T, HQ, HK, D, e)
     return {"value": round(layer_bytes / t / 1e9, 2), "unit": "GB/s", "cores": threads,
-            "cpu_model": model, "kind": "port",
+            "cores_note": _cpu_threads_note(), "cpu_model": model, "kind": "port",
             "sample": f"one layer of config 4 (2 RMSNorm + q/k RoPE, fwd + autograd bwd) on "
                       f"{B} of its 8 rows (T={T}), fp32 PyTorch eager (HF Qwen2RMSNorm / apply_rotary_pos_emb "
                       f"restated), median of {len(times)} reps, {t * 1e3:.1f} ms per layer; "
