@@ -15,7 +15,9 @@
 
 #include "probe.h"
 
-namespace {
+// Named (not anonymous) so that the kernels carry "esep" in their symbol names, as the library's
+// do (the profiles select kernels by that).
+namespace esep_probe {
 
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __amdgpu_buffer_rsrc_t rsrc_t;
@@ -97,7 +99,10 @@ kern_t pick(int mode, int u) {
   return nullptr;
 }
 
-}  // namespace
+}  // namespace esep_probe
+
+using esep_probe::kern_t;
+using esep_probe::pick;
 
 extern "C" {
 
