@@ -520,7 +520,8 @@ constexpr int kBwdPipeThreads = 256;
 // 13.7 us, arithmetic without the partials' store 14.3 us.
 //
 // FIX fixes the call's optional parts at compile time: 1 = saved rstd, dx only, with the weight
-// gradient; 2 = the same without it; 0 reads them from the arguments.
+// gradient; 2 = the same without it; 3 = rstd recomputed from x, dx only, with the weight
+// gradient; 0 reads them from the arguments.
 template <int NV, typename TX, typename TDY, typename TO, int FIX>
 __device__ __forceinline__ void bwd_rows_pipe(const BwdArgs& a, float* lds) {
   constexpr int G = kWave;  // one wavefront per row: every row reduction is a DPP wave sum
@@ -537,8 +538,8 @@ __device__ __forceinline__ void bwd_rows_pipe(const BwdArgs& a, float* lds) {
   // rows of the block's groups (block-uniform: the groups of a block differ by at most one row;
   // a group's surplus rows read 0 and store nothing), at least 1
   const int iters_blk = (rows - (int)blockIdx.x * gpb + step - 1) / step;
-  const bool want_dw = FIX == 1 ? true : FIX == 2 ? false : a.part != nullptr;
-  const bool has_rstd = FIX != 0 || a.rstd != nullptr;
+  const bool want_dw = (FIX == 1 || FIX == 3) ? true : FIX == 2 ? false : a.part != nullptr;
+  const bool has_rstd = (FIX == 1 || FIX == 2) ? true : FIX == 3 ? false : a.rstd != nullptr;
   const bool has_dr = FIX == 0 && a.dr != nullptr;
   const bool has_dx = FIX != 0 || a.dx != nullptr;
   const float inv_n = 1.0f / (float)n;

@@ -22,12 +22,18 @@ static hipError_t bwd_nv(const BwdArgs& a, int nv, dim3 grid, dim3 block, size_t
   if (a.fast == 1) {
     if (block.x != (unsigned)kBwdPipeThreads || a.gpb != kBwdPipeThreads / kWave || a.wpr != 1)
       return hipErrorInvalidValue;
-    // saved rstd and dx only (the common call) run a form with those parts fixed
+    // saved rstd and dx only (the common call) run a form with those parts fixed, and so does
+    // dx only with the weight gradient and rstd recomputed (config 4 with rstd recomputed: 16.25
+    // us per launch in the trace with the parts read from the arguments)
     const bool common = a.rstd != nullptr && a.dr == nullptr && a.dx != nullptr;
-    const int fix = common ? (a.part != nullptr ? 1 : 2) : 0;
+    const bool recompute = a.rstd == nullptr && a.dr == nullptr && a.dx != nullptr && a.part != nullptr;
+    const int fix = common ? (a.part != nullptr ? 1 : 2) : recompute ? 3 : 0;
     if (fix == 1) {
       if (nv == 2) hipLaunchKernelGGL((k_rmsnorm_bwd_pipe<2, TX, TDY, TO, 1>), grid, block, lds, s, a);
       else hipLaunchKernelGGL((k_rmsnorm_bwd_pipe<3, TX, TDY, TO, 1>), grid, block, lds, s, a);
+    } else if (fix == 3) {
+      if (nv == 2) hipLaunchKernelGGL((k_rmsnorm_bwd_pipe<2, TX, TDY, TO, 3>), grid, block, lds, s, a);
+      else hipLaunchKernelGGL((k_rmsnorm_bwd_pipe<3, TX, TDY, TO, 3>), grid, block, lds, s, a);
     } else if (fix == 2) {
       if (nv == 2) hipLaunchKernelGGL((k_rmsnorm_bwd_pipe<2, TX, TDY, TO, 2>), grid, block, lds, s, a);
       else hipLaunchKernelGGL((k_rmsnorm_bwd_pipe<3, TX, TDY, TO, 2>), grid, block, lds, s, a);
