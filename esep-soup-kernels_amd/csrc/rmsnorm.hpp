@@ -685,7 +685,7 @@ __device__ __forceinline__ void bwd_rows_pipe(const BwdArgs& a, float* lds) {
     const rsrc_t rp = make_rsrc(a.part + (int64_t)blockIdx.x * n, (uint32_t)n * 4u);
     constexpr int nthr = gpb * G;
 #pragma unroll
-    for (int j = 0; j < (NV * G * 8) / (2 * nthr); ++j) {
+    for (int j = 0; j < (NV * G * 8 + 2 * nthr - 1) / (2 * nthr); ++j) {  // every pair of the slot
       const int c = 2 * (int)threadIdx.x + 2 * nthr * j;
       if (c < n) {
         float2 t = *reinterpret_cast<const float2*>(lds + c);
