@@ -161,14 +161,18 @@ __device__ __forceinline__ void fwd_rows(const FwdArgs& a, float* red) {
   ss = row_sum(ss, a.wpr, red);
   const float inv = inv_rms(ss, n, a.eps);
 
+  // every weight chunk is loaded before the first y store, so no weight load waits behind a
+  // store in the one in-order counter of loads and stores (config 5: 163.2 -> 162.3 us)
   const Span rw = make_span(a.w, (uint32_t)n * 4u);
   const Span ry = row_rsrc<TY>(a.y, row, a.ld_y, n, ok);
+  float w8[NV][8];
+#pragma unroll
+  for (int k = 0; k < NV; ++k) bload<VEC, float, kCached>(rw, (tg + k * G) * 32, w8[k]);
 #pragma unroll
   for (int k = 0; k < NV; ++k) {
-    float w8[8], o[8];
-    bload<VEC, float, kCached>(rw, (tg + k * G) * 32, w8);
+    float o[8];
 #pragma unroll
-    for (int e = 0; e < 8; ++e) o[e] = w8[e] * (v[k][e] * inv);
+    for (int e = 0; e < 8; ++e) o[e] = w8[k][e] * (v[k][e] * inv);
     bstore<VEC, TY>(ry, (tg + k * G) * 8 * sizeof(TY), o);
   }
   if (a.rstd != nullptr && ok && tg == 0) a.rstd[row] = inv;
