@@ -98,6 +98,27 @@ def test_config4_deferred_dgamma_equals_per_call():
         assert torch.equal(fused.dx[i], batched.dx[i]), i
 
 
+def test_config4_recomputed_rstd_equals_saved():
+    """The bench's two rstd legs at config 4 (one layer, deferred weight gradient): the
+    backward's form for rstd recomputed from x (dx only, with the weight gradient) gives the
+    saved-rstd form's dx and dw bit for bit, since it recomputes rstd with the forward's own
+    arithmetic."""
+    bench = _bench()
+    cfg = dict(bench.CFG4, layers=1)
+    dev = torch.device(DEV)
+    saved = bench.Body(cfg, True, dev)
+    recomputed = bench.Body(cfg, False, dev)
+    saved.step()
+    recomputed.step()
+    torch.cuda.synchronize()
+    for i in range(2 * cfg["layers"] + 1):
+        assert recomputed.rstd[i] is None and saved.rstd[i] is not None
+        assert torch.equal(saved.x[i], recomputed.x[i])  # same seeded inputs
+        assert torch.equal(saved.y[i], recomputed.y[i]), i
+        assert torch.equal(saved.dx[i], recomputed.dx[i]), i
+        assert torch.equal(saved.dw[i], recomputed.dw[i]), i
+
+
 def test_config4_norm_api_full_size():
     """The public rmsnorm() API at config 4's norm shape ([8, 1024, 1536] bf16, trainable fp32
     weight 1 + 0.02 N(0, 1)): y and dx on sampled rows, dw over all rows."""
