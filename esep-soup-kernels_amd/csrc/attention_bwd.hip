@@ -321,17 +321,27 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dq_dma(const AttnBwdArg
   };
 
   if (ntiles > 0) issue(kv[0][0], kv[0][1], start);
-  for (int t = 0; t < ntiles; ++t) {
+  // Tile t sits in buffer B = t % 2, the loop unrolled by two so that B is a constant and the
+  // tiles' LDS addresses fold into the reads' immediate offsets, as in the forward
+  // (config-5-like backward 4.70 -> 4.66 ms, the same bits). The dK / dV kernel is left rolled:
+  // unrolled it spills at its 256 registers and measured 4.5% slower.
+  auto tile = [&](int t, auto bc) {
+    constexpr int B = decltype(bc)::value;
     // this wavefront's DMA of tile t has landed; the barrier publishes every wavefront's rows
     // and certifies that tile t - 1, in the other buffer, is consumed
     __builtin_amdgcn_s_waitcnt(kWaitVm0);
     __syncthreads();
-    if (t + 1 < ntiles) issue(kv[(t + 1) & 1][0], kv[(t + 1) & 1][1], start + (t + 1) * BN);
+    if (t + 1 < ntiles) issue(kv[B ^ 1][0], kv[B ^ 1][1], start + (t + 1) * BN);
     const int kt = start + t * BN;
-    if (!wave_live || kt > wq_last) continue;
-    dq_tile_swz<T>(kv[t & 1][0], kv[t & 1][1], kt, qw0, qi, lane, a.scale_log2, lse2, delta, qb,
-                   db, dqa);
+    if (!wave_live || kt > wq_last) return;
+    dq_tile_swz<T>(kv[B][0], kv[B][1], kt, qw0, qi, lane, a.scale_log2, lse2, delta, qb, db, dqa);
+  };
+  int t = 0;
+  for (; t + 1 < ntiles; t += 2) {
+    tile(t, std::integral_constant<int, 0>{});
+    tile(t + 1, std::integral_constant<int, 1>{});
   }
+  if (t < ntiles) tile(t, std::integral_constant<int, 0>{});
   if (!qok) return;
   store_rows_t<T, D>(static_cast<T*>(b.dq) + (int64_t)qi * b.dq_rs + (int64_t)h * D, dqa, hi,
                      a.scale);
