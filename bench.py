@@ -1100,7 +1100,7 @@ def _cpu_time(fn, budget_s, min_reps=5):
 def cpu_configs(cfg5, budget_s=2.0):
     """The same PyTorch-eager fp32 HF path on the host cores for configs 1-3 (whole) and config
     5 (its longest-sequence share: one 4096-token sequence at H = 3584, 28/4 heads), forward +
-    autograd backward; GB/s with e = 4 (BASELINE.md's CPU rule)."""
+    autograd backward; GB/s from the same byte formulas with 4-byte (fp32) elements."""
     import torch
 
     from oracle import hf_eager
