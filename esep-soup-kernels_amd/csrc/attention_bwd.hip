@@ -567,24 +567,36 @@ __global__ __launch_bounds__(64 * NW, 2) void k_attn_bwd_dkdv(const AttnBwdArgs 
           sb_[i / 8][i % 8] = (T)(p * (dp[i] - dr[e]));
         }
       }
+      __builtin_amdgcn_sched_barrier(0);
       __builtin_amdgcn_s_setprio(1);
-      // dV^T += dO^T P and dK^T += Q^T dS, queries in the permuted order of pb / sb_
-#pragma unroll
-      for (int md = 0; md < D / 32; ++md)
-#pragma unroll
-        for (int c2 = 0; c2 < 2; ++c2) {
-          const int rb = 32 * qh + 16 * c2;
-          V8 dot, qt_;
-          if constexpr (DMA) {
-            dot = trd.template read<V8>(dsb, rb, md);
-            qt_ = trd.template read<V8>(qsb, rb, md);
-          } else {
-            dot = ld_tr<V8, RP>(reinterpret_cast<const T*>(dsb), rb, 32 * md, lane);
-            qt_ = ld_tr<V8, RP>(reinterpret_cast<const T*>(qsb), rb, 32 * md, lane);
-          }
-          dva[md] = Mfma<T>::run(dot, pb[c2], dva[md]);
-          dka[md] = Mfma<T>::run(qt_, sb_[c2], dka[md]);
+      // dV^T += dO^T P and dK^T += Q^T dS, queries in the permuted order of pb / sb_: operand
+      // pair i = (md, c2) = (i / 2, i % 2) read RB pairs ahead, pinned by scheduling barriers
+      // (the compiler kept one pair ahead: config-5-like backward 4.66 -> 4.56 ms, the same
+      // bits; three ahead, or the first pairs read before the exponentials, spill at 256
+      // registers)
+      constexpr int RB = 2;
+      V8 dotb[RB], qtb[RB];
+      auto rd = [&](int i, int slot) {
+        const int md = i >> 1, rb = 32 * qh + 16 * (i & 1);
+        if constexpr (DMA) {
+          dotb[slot] = trd.template read<V8>(dsb, rb, md);
+          qtb[slot] = trd.template read<V8>(qsb, rb, md);
+        } else {
+          dotb[slot] = ld_tr<V8, RP>(reinterpret_cast<const T*>(dsb), rb, 32 * md, lane);
+          qtb[slot] = ld_tr<V8, RP>(reinterpret_cast<const T*>(qsb), rb, 32 * md, lane);
         }
+      };
+#pragma unroll
+      for (int i = 0; i < RB; ++i) rd(i, i);
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int i = 0; i < 2 * (D / 32); ++i) {
+        const int md = i >> 1, c2 = i & 1;
+        dva[md] = Mfma<T>::run(dotb[i % RB], pb[c2], dva[md]);
+        dka[md] = Mfma<T>::run(qtb[i % RB], sb_[c2], dka[md]);
+        if (i + RB < 2 * (D / 32)) rd(i + RB, i % RB);
+        __builtin_amdgcn_sched_barrier(0);
+      }
       __builtin_amdgcn_s_setprio(0);
     }
   }
