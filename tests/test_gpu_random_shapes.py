@@ -1,0 +1,151 @@
+"""Seeded random shapes through the public API of the three operations (norm, RoPE, varlen
+attention), each case against the fp64 CPU oracle at the bars of the fixed-shape tests:
+
+  rmsnorm   y, dx atol 2e-3 / rtol 1e-2 (16-bit) or 1e-5 (fp32); dw 1e-4 of max |dw|
+  rope      q, k forward (sign +1) and dq, dk backward (sign -1), the same bars as rmsnorm's y
+  attention o within atol 1e-2 (bf16) / 2e-3 (fp16) + rtol 1e-2; dq, dk, dv within that atol
+            times the gradient's largest magnitude + rtol 1e-2 + 1e-5
+
+The shapes are drawn per case from numpy's default_rng(seed) (the case id is the seed), so a
+failure names a reproducible case: ragged widths and lengths, empty sequences, a max_seqlen
+larger than the longest sequence, odd query-head groups. ESEP_RANDOM_SHAPES_SCALE=k runs k times
+as many seeds per operation (a wider sweep by hand; 1 by default)."""
+
+import os
+
+import numpy as np
+import pytest
+import torch
+
+from _util import DEV, STORE, assert_close, np64
+from oracle import attention_ref as aref
+from oracle import norm_rope_ref as ref
+
+pytestmark = pytest.mark.gpu
+
+SCALE = max(1, int(os.environ.get("ESEP_RANDOM_SHAPES_SCALE", "1")))
+
+
+def _seeds(first, count):
+    """Case seeds: count per operation, scaled; the scaled ones continue past the defaults'
+    range of every operation (10000 apart)."""
+    return list(range(first, first + count)) + [first + 10000 + i for i in range(count * (SCALE - 1))]
+
+
+EPS = 1e-6
+DTYPES = [torch.bfloat16, torch.float16, torch.float32]
+
+
+def _nr():
+    from solution.body import norm_rope
+
+    return norm_rope
+
+
+def _tensor(rng, shape, dtype, scale=1.0):
+    return torch.from_numpy(rng.standard_normal(shape) * scale).to(torch.float32).to(dtype).to(DEV)
+
+
+def _norm_case(seed):
+    rng = np.random.default_rng(seed)
+    n = int(rng.choice([int(rng.integers(1, 200)), int(rng.integers(200, 4097)),
+                        int(rng.integers(4097, 16385)), 1536, 3584]))
+    rows = int(rng.integers(1, max(2, min(2500, 4_000_000 // n))))
+    dtype = DTYPES[int(rng.integers(3))]
+    recompute = bool(rng.integers(2))
+    return rng, rows, n, dtype, recompute
+
+
+@pytest.mark.parametrize("seed", _seeds(100, 16))
+def test_random_rmsnorm(seed):
+    nr = _nr()
+    rng, rows, n, dtype, recompute = _norm_case(seed)
+    print(f"seed {seed}: rows={rows} n={n} {dtype} recompute_rstd={recompute}")
+    x = _tensor(rng, (rows, n), dtype).requires_grad_()
+    w = (1 + 0.02 * _tensor(rng, (n,), torch.float32)).requires_grad_()
+    dy = _tensor(rng, (rows, n), dtype)
+    y = nr.rmsnorm(x, w, EPS, recompute_rstd=recompute)
+    dx, dw = torch.autograd.grad(y, [x, w], dy)
+    y64, _ = ref.rmsnorm_fwd(np64(x), np64(w), EPS, STORE[dtype])
+    dx64, dw64 = ref.rmsnorm_bwd(np64(dy), np64(x), np64(w), EPS)
+    lp = dtype != torch.float32
+    atol, rtol = (2e-3, 1e-2) if lp else (1e-5, 1e-5)
+    assert_close(np64(y), y64, atol, rtol, "y")
+    assert_close(np64(dx), ref.round_to(dx64, STORE[dtype]), atol, rtol, "dx")
+    assert_close(np64(dw), dw64, 1e-4 * np.abs(dw64).max(), 1e-4, "dw")
+
+
+def _lengths(rng, n_seq, hi, p_empty=0.15):
+    lens = [0 if rng.random() < p_empty else int(rng.integers(1, hi)) for _ in range(n_seq)]
+    if max(lens) == 0:
+        lens[0] = int(rng.integers(1, hi))
+    return lens
+
+
+@pytest.mark.parametrize("seed", _seeds(200, 12))
+def test_random_rope(seed):
+    nr = _nr()
+    rng = np.random.default_rng(seed)
+    hq, hk = [(12, 2), (28, 4), (4, 4), (6, 1), (16, 8)][int(rng.integers(5))]
+    d = [64, 128, 256][int(rng.integers(3))]
+    dtype = DTYPES[int(rng.integers(3))]
+    kind = ["positions", "cu_seqlens", "large_positions"][int(rng.integers(3))]
+    inv_freq = nr.default_inv_freq(d, 1e6, DEV)
+    if kind == "cu_seqlens":
+        lens = _lengths(rng, int(rng.integers(1, 12)), 600)
+        cu = torch.tensor(aref.cu_from_lengths(lens), dtype=torch.int32)
+        pos_np = ref.positions_from_cu_seqlens(cu.numpy())
+        T = int(cu[-1])
+    else:
+        T = int(rng.integers(1, 3000))
+        top = 32768 if kind == "large_positions" else 1024
+        pos_np = rng.integers(0, top, T).astype(np.int64)
+    print(f"seed {seed}: T={T} heads {hq}/{hk} D={d} {dtype} {kind}")
+    q = _tensor(rng, (T, hq, d), dtype).requires_grad_()
+    k = _tensor(rng, (T, hk, d), dtype).requires_grad_()
+    if kind == "cu_seqlens":
+        qo, ko = nr.rope(q, k, None, inv_freq, cu_seqlens=cu.to(DEV))
+    else:
+        qo, ko = nr.rope(q, k, torch.from_numpy(pos_np).to(DEV), inv_freq)
+    f = inv_freq.cpu().numpy()
+    lp = dtype != torch.float32
+    atol, rtol = (2e-3, 1e-2) if lp else (1e-5, 1e-5)
+    assert_close(np64(qo), ref.rope_fwd(np64(q), pos_np, f, store=STORE[dtype]), atol, rtol, "q")
+    assert_close(np64(ko), ref.rope_fwd(np64(k), pos_np, f, store=STORE[dtype]), atol, rtol, "k")
+    gq, gk = _tensor(rng, qo.shape, dtype), _tensor(rng, ko.shape, dtype)
+    dq, dk = torch.autograd.grad([qo, ko], [q, k], [gq, gk])
+    assert_close(np64(dq), ref.rope_fwd(np64(gq), pos_np, f, -1.0, store=STORE[dtype]), atol, rtol,
+                 "dq")
+    assert_close(np64(dk), ref.rope_fwd(np64(gk), pos_np, f, -1.0, store=STORE[dtype]), atol, rtol,
+                 "dk")
+
+
+@pytest.mark.parametrize("seed", _seeds(300, 12))
+def test_random_attention(seed):
+    from solution.body import _hip
+
+    rng = np.random.default_rng(seed)
+    lens = _lengths(rng, int(rng.integers(1, 7)), 330)
+    HQ, HK = [(2, 1), (4, 2), (6, 2), (8, 8), (12, 2), (7, 1)][int(rng.integers(6))]
+    D = [64, 128][int(rng.integers(2))]
+    dtype = [torch.bfloat16, torch.float16][int(rng.integers(2))]
+    max_seqlen = max(lens) + int(rng.integers(0, 40))  # any bound >= the longest sequence
+    print(f"seed {seed}: lengths {lens} heads {HQ}/{HK} D={D} {dtype} max_seqlen={max_seqlen}")
+    T = sum(lens)
+    q, do = _tensor(rng, (T, HQ, D), dtype), _tensor(rng, (T, HQ, D), dtype)
+    k, v = _tensor(rng, (T, HK, D), dtype), _tensor(rng, (T, HK, D), dtype)
+    cu = torch.tensor(aref.cu_from_lengths(lens), dtype=torch.int32)
+    scale = D ** -0.5
+    o = torch.full_like(q, float("nan"))
+    lse = torch.full((HQ, T), float("nan"), device=DEV)
+    _hip.attn_fwd(q, k, v, o, cu.to(DEV), max_seqlen, scale, lse=lse)
+    dq, dk, dv = (torch.full_like(t, float("nan")) for t in (q, k, v))
+    _hip.attn_bwd(q, k, v, o, do, lse, dq, dk, dv, cu.to(DEV), max_seqlen, scale)
+    cu_np = cu.numpy()
+    o64, lse64 = aref.attn_fwd(np64(q), np64(k), np64(v), cu_np, scale)
+    atol = 1e-2 if dtype == torch.bfloat16 else 2e-3
+    assert_close(np64(o), o64, atol, 1e-2, "o")
+    np.testing.assert_allclose(np64(lse), lse64, atol=1e-4, rtol=1e-5)
+    want = aref.attn_bwd(np64(q), np64(k), np64(v), np64(do), cu_np, scale)
+    for name, got, w64 in zip(("dq", "dk", "dv"), (dq, dk, dv), want):
+        assert_close(np64(got), w64, atol * np.abs(w64).max() + 1e-5, 1e-2, name)
