@@ -1,8 +1,10 @@
 // Instantiations and launch dispatch of the RMSNorm backward kernel and of the weight-gradient
 // reduction. Supported (x, dy, dx) element types:
 //   x fp32 (the fp32 residual): dy fp32/fp16/bf16, dx fp32/fp16/bf16
-//   x fp16 (saved fp16 output or fp16 input): dy fp16/fp32, dx fp16/fp32
-//   x bf16 (saved bf16 output or bf16 input): dy bf16/fp32, dx bf16/fp32
+//   x fp16 (saved fp16 output or fp16 input): dy fp16/fp32, dx fp16/fp32; with dy fp16 also
+//          dx bf16 (the reference API's saved-output backward with a bf16 residual delta)
+//   x bf16 (saved bf16 output or bf16 input): dy bf16/fp32, dx bf16/fp32; with dy bf16 also
+//          dx fp16 (the same with an fp16 delta)
 // A call that writes no low-precision dx uses dx type fp32 (nothing is stored through it).
 #include "rmsnorm.hpp"
 
@@ -67,9 +69,11 @@ static hipError_t bwd_o(const BwdArgs& a, int o_dt, int nv, dim3 g, dim3 b, size
                         hipStream_t s, bool* sup) {
   *sup = true;
   if (o_dt == 0) return bwd_nv<TX, TDY, float>(a, nv, g, b, lds, s);
-  constexpr int xc = kCode<TX>;
-  if (o_dt == 1 && (xc == 0 || xc == 1)) return bwd_nv<TX, TDY, _Float16>(a, nv, g, b, lds, s);
-  if (o_dt == 2 && (xc == 0 || xc == 2)) return bwd_nv<TX, TDY, __bf16>(a, nv, g, b, lds, s);
+  constexpr int xc = kCode<TX>, dc = kCode<TDY>;
+  if constexpr (xc == 0 || xc == 1 || (xc == 2 && dc == 2))
+    if (o_dt == 1) return bwd_nv<TX, TDY, _Float16>(a, nv, g, b, lds, s);
+  if constexpr (xc == 0 || xc == 2 || (xc == 1 && dc == 1))
+    if (o_dt == 2) return bwd_nv<TX, TDY, __bf16>(a, nv, g, b, lds, s);
   *sup = false;
   return hipErrorInvalidValue;
 }

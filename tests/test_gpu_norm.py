@@ -266,6 +266,32 @@ def test_add_rmsnorm_save_output(T, kind):
     assert err(np64(g_new[1]), np64(want))[1] < 5e-3
 
 
+@pytest.mark.parametrize("delta_dt,out_dt", [(torch.float16, torch.bfloat16),
+                                              (torch.bfloat16, torch.float16)],
+                         ids=["fp16_delta_bf16_y", "bf16_delta_fp16_y"])
+@pytest.mark.parametrize("kind", ["regular", "qwen_like"])
+def test_add_rmsnorm_save_output_mixed_16bit(delta_dt, out_dt, kind):
+    """save_output with a delta of the other 16-bit type than y: the backward reads the saved y
+    (one 16-bit type) and writes the delta's gradient in the other. The forward is bitwise that
+    of the r_out mode; the gradients are within the saved-y bars of the fp64 closed form (2e-3 /
+    5e-3 of their largest magnitude for an fp16 y, 8 times that for a bf16 y)."""
+    g = gen(77)
+    T = 300
+    w = _weight(kind, g)
+    r_in = _rows(T, False, g).view(1, T, H)
+    delta = torch.randn(1, T, H, generator=g).to(delta_dt).to(DEV)
+    gys = [torch.randn(1, T, H, generator=g).to(out_dt).to(DEV) for _ in range(2)]
+    gr = torch.randn(1, T, H, generator=g).to(DEV)
+    r0, y0, _ = _norm_grads(r_in, delta, w, gys, gr, False, out_dt)
+    r1, y1, (d_rin, d_delta) = _norm_grads(r_in, delta, w, gys, gr, True, out_dt)
+    assert torch.equal(r0, r1) and torch.equal(y0, y1)
+    assert d_rin.dtype == torch.float32 and d_delta.dtype == delta_dt
+    want = _ref_grads_f64(r_in, delta, w, gys, gr)
+    k = 8 if out_dt == torch.bfloat16 else 1
+    assert err(np64(d_rin), np64(want))[1] < 2e-3 * k
+    assert err(np64(d_delta), np64(want))[1] < 5e-3 * k
+
+
 def test_add_rmsnorm_save_output_precision():
     """Reference :354-379: realistic magnitudes and outliers, y-based backward error bounds."""
     T = 1000

@@ -17,7 +17,7 @@ import numpy as np
 import pytest
 import torch
 
-from _util import DEV, STORE, assert_close, np64
+from _util import DEV, STORE, assert_close, err, np64
 from oracle import attention_ref as aref
 from oracle import norm_rope_ref as ref
 
@@ -73,6 +73,53 @@ def test_random_rmsnorm(seed):
     assert_close(np64(y), y64, atol, rtol, "y")
     assert_close(np64(dx), ref.round_to(dx64, STORE[dtype]), atol, rtol, "dx")
     assert_close(np64(dw), dw64, 1e-4 * np.abs(dw64).max(), 1e-4, "dw")
+
+
+@pytest.mark.parametrize("seed", _seeds(400, 12))
+def test_random_add_rmsnorm(seed):
+    """The reference API's add_rmsnorm (residual add, fan-out, save_output) on random shapes:
+    r_out exact, y at the bar above; d_r_in, d_delta and the weight's gradient against the fp64
+    closed form (relative 2e-3 / 5e-3 of their largest magnitude on the saved-y backward, as its
+    fixed-shape tests, 8 times that for a bf16 y). A delta of the other 16-bit type than y's
+    exercises the backward kernel's mixed forms (x and dy fp16, dx bf16 and the reverse)."""
+    nr = _nr()
+    rng = np.random.default_rng(seed)
+    n = int(rng.choice([int(rng.integers(1, 300)), int(rng.integers(300, 16385)), 1536, 3584]))
+    T = int(rng.integers(1, max(2, min(2000, 3_000_000 // n))))
+    delta_dt = [None, torch.float16, torch.bfloat16, torch.float32][int(rng.integers(4))]
+    out_dt = DTYPES[int(rng.integers(3))]
+    n_out = int(rng.integers(1, 4))
+    save_output = bool(rng.integers(2))
+    print(f"seed {seed}: T={T} n={n} delta {delta_dt} y {out_dt} n_out={n_out} "
+          f"save_output={save_output}")
+    r_in = _tensor(rng, (T, n), torch.float32, 3.0).requires_grad_()
+    delta = None if delta_dt is None else _tensor(rng, (T, n), delta_dt).requires_grad_()
+    w = torch.nn.Parameter(1 + 0.1 * _tensor(rng, (n,), torch.float32))
+    r_out, ys = nr.add_rmsnorm(r_in, delta, w, EPS, out_dt, n_out=n_out, save_output=save_output)
+    ys = (ys,) if n_out == 1 else ys
+    d_np = None if delta is None else np64(delta)
+    r64, y64, _, _ = ref.add_rmsnorm_fwd(np64(r_in), d_np, np64(w.detach()), EPS, STORE[out_dt])
+    assert_close(np64(r_out), r64, 0, 0, "r_out")
+    lp = out_dt != torch.float32
+    assert_close(np64(ys[0]), y64, 2e-3 if lp else 1e-5, 1e-2 if lp else 1e-5, "y")
+    gys = [_tensor(rng, (T, n), out_dt) for _ in range(n_out)]
+    gr = _tensor(rng, (T, n), torch.float32)
+    torch.autograd.backward([r_out, *ys], [gr, *gys])
+    dr64, dw64 = ref.add_rmsnorm_bwd([np64(g) for g in gys], np64(gr), r64, np64(w.detach()), EPS)
+    from_y = save_output and delta is not None and lp  # the backward from the saved y
+    # xhat = y / w there: the bars of the fp16 tests, 8x for a bf16 y (3 fewer mantissa bits)
+    yk = 8 if out_dt == torch.bfloat16 else 1
+    if from_y:
+        assert err(np64(r_in.grad), dr64)[1] < 2e-3 * yk
+        assert err(np64(delta.grad), dr64)[1] < 5e-3 * yk
+    else:
+        assert_close(np64(r_in.grad), dr64, 1e-4 * np.abs(dr64).max(), 1e-4, "d_r_in")
+        if delta is not None:
+            assert_close(np64(delta.grad), ref.round_to(dr64, STORE[delta_dt]),
+                         2e-3 * np.abs(dr64).max() if delta_dt != torch.float32 else 1e-5,
+                         1e-2 if delta_dt != torch.float32 else 1e-4, "d_delta")
+    assert_close(np64(w.grad), dw64, 2e-3 * yk * np.abs(dw64).max() if from_y else
+                 1e-4 * np.abs(dw64).max(), 1e-4, "w.grad")
 
 
 def _lengths(rng, n_seq, hi, p_empty=0.15):
