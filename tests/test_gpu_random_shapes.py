@@ -167,6 +167,84 @@ def test_random_rope(seed):
                  "dk")
 
 
+@pytest.mark.parametrize("seed", _seeds(500, 12))
+def test_random_rope_layouts(seed):
+    """rope on q / k sliced from one fused [T, (HQ + 2 HK) D] projection buffer, with or without
+    the LoRA term q_delta (its gradient bitwise q's), and rope_bhsd on the padded [B, H, S, D]
+    layout (contiguous or HF's transposed view; positions implicit, per row or one broadcast
+    row), forward and backward against the oracle."""
+    nr = _nr()
+    rng = np.random.default_rng(seed)
+    hq, hk = [(12, 2), (28, 4), (4, 4), (6, 1)][int(rng.integers(4))]
+    d = [64, 128, 256][int(rng.integers(3))]
+    dtype = DTYPES[int(rng.integers(3))]
+    inv_freq = nr.default_inv_freq(d, 1e6, DEV)
+    f = inv_freq.cpu().numpy()
+    atol, rtol = (2e-3, 1e-2) if dtype != torch.float32 else (1e-5, 1e-5)
+    st = STORE[dtype]
+    if rng.integers(2):
+        T = int(rng.integers(1, 2500))
+        with_delta = bool(rng.integers(2))
+        print(f"seed {seed}: fused qkv T={T} heads {hq}/{hk} D={d} {dtype} q_delta={with_delta}")
+        qkv = _tensor(rng, (T, (hq + 2 * hk) * d), dtype).requires_grad_()
+        qv = qkv[:, : hq * d].view(T, hq, d)
+        kv = qkv[:, hq * d:(hq + hk) * d].view(T, hk, d)
+        qd = _tensor(rng, (T, hq * d), dtype, 0.3).requires_grad_() if with_delta else None
+        pos = rng.integers(0, 4096, T).astype(np.int64)
+        qo, ko = nr.rope(qv, kv, torch.from_numpy(pos).to(DEV), inv_freq, qd)
+        dq_np = None if qd is None else np64(qd)
+        assert_close(np64(qo), ref.rope_fwd(np64(qv), pos, f, delta=dq_np, store=st), atol, rtol, "q")
+        assert_close(np64(ko), ref.rope_fwd(np64(kv), pos, f, store=st), atol, rtol, "k")
+        gq, gk = _tensor(rng, qo.shape, dtype), _tensor(rng, ko.shape, dtype)
+        leaves = [qkv] + ([qd] if qd is not None else [])
+        grads = torch.autograd.grad([qo, ko], leaves, [gq, gk])
+        gqkv = grads[0]
+        assert_close(np64(gqkv[:, : hq * d]).reshape(T, hq, d),
+                     ref.rope_fwd(np64(gq), pos, f, -1.0, store=st), atol, rtol, "dq")
+        assert_close(np64(gqkv[:, hq * d:(hq + hk) * d]).reshape(T, hk, d),
+                     ref.rope_fwd(np64(gk), pos, f, -1.0, store=st), atol, rtol, "dk")
+        assert not gqkv[:, (hq + hk) * d:].any()  # v's columns get no gradient
+        if qd is not None:
+            assert torch.equal(grads[1], gqkv[:, : hq * d])
+        return
+    B, S = int(rng.integers(1, 5)), int(rng.integers(1, 700))
+    view = bool(rng.integers(2))
+    pos_kind = ["implicit", "per_row", "broadcast"][int(rng.integers(3))]
+    print(f"seed {seed}: bhsd B={B} S={S} heads {hq}/{hk} D={d} {dtype} hf_view={view} {pos_kind}")
+    if view:
+        q = _tensor(rng, (B, S, hq * d), dtype).requires_grad_()
+        k = _tensor(rng, (B, S, hk * d), dtype).requires_grad_()
+        qv, kv = q.view(B, S, hq, d).transpose(1, 2), k.view(B, S, hk, d).transpose(1, 2)
+    else:
+        q = _tensor(rng, (B, hq, S, d), dtype).requires_grad_()
+        k = _tensor(rng, (B, hk, S, d), dtype).requires_grad_()
+        qv, kv = q, k
+    if pos_kind == "implicit":
+        pid, posr = None, np.tile(np.arange(S), B)
+    elif pos_kind == "per_row":
+        p = rng.integers(0, 8192, (B, S)).astype(np.int64)
+        pid, posr = torch.from_numpy(p).to(DEV), p.reshape(-1)
+    else:
+        p = rng.integers(0, 8192, (1, S)).astype(np.int64)
+        pid, posr = torch.from_numpy(p).to(DEV), np.tile(p[0], B)
+    qo, ko = nr.rope_bhsd(qv, kv, inv_freq, pid)
+
+    def tok(t, h):  # [B, H, S, D] -> token-major [B S, H, D]
+        return np64(t.transpose(1, 2)).reshape(B * S, h, d)
+
+    def bhsd(a, h):
+        return a.reshape(B, S, h, d).transpose(0, 2, 1, 3)
+
+    assert_close(np64(qo), bhsd(ref.rope_fwd(tok(qv, hq), posr, f, store=st), hq), atol, rtol, "q")
+    assert_close(np64(ko), bhsd(ref.rope_fwd(tok(kv, hk), posr, f, store=st), hk), atol, rtol, "k")
+    gq, gk = _tensor(rng, tuple(qo.shape), dtype), _tensor(rng, tuple(ko.shape), dtype)
+    dq, dk = torch.autograd.grad([qo, ko], [qv, kv], [gq, gk])
+    assert_close(np64(dq), bhsd(ref.rope_fwd(tok(gq, hq), posr, f, -1.0, store=st), hq), atol, rtol,
+                 "dq")
+    assert_close(np64(dk), bhsd(ref.rope_fwd(tok(gk, hk), posr, f, -1.0, store=st), hk), atol, rtol,
+                 "dk")
+
+
 @pytest.mark.parametrize("seed", _seeds(300, 12))
 def test_random_attention(seed):
     from solution.body import _hip
