@@ -122,6 +122,79 @@ def test_random_add_rmsnorm(seed):
                  1e-4 * np.abs(dw64).max(), 1e-4, "w.grad")
 
 
+@pytest.mark.parametrize("seed", _seeds(450, 10))
+def test_random_deferred_weight_grad_graphs(seed):
+    """Random chains of rmsnorm / add_rmsnorm calls over a small pool of trainable weights (so
+    that a weight is shared by several norms of one pass), fp32 or bf16 parameters, some calls
+    on a derived weight (p * 0.5: autograd's chain rule, per call), one loss.backward(): the
+    inputs' gradients bit for bit, a weight used by one norm bit for bit, and a shared weight's
+    .grad within the rounding of summing its contributions in another order (autograd fixes no
+    order: the deferred ones are added at the end of the pass, the engine adds the per-call
+    ones as they arrive): |deferred - per call| <= uses * eps(dtype) * sum |contribution|, the
+    contributions measured in a third run with each use on a weight tensor of its own."""
+    nr = _nr()
+    rng = np.random.default_rng(seed)
+    n = [64, 1000, 1536, 3584][int(rng.integers(4))]
+    T = int(rng.integers(1, 400))
+    n_params = int(rng.integers(1, 4))
+    p_dt = [torch.float32, torch.bfloat16][int(rng.integers(2))]
+    calls = [(int(rng.integers(2)), int(rng.integers(n_params)), bool(rng.random() < 0.2),
+              bool(rng.integers(2))) for _ in range(int(rng.integers(2, 7)))]
+    print(f"seed {seed}: n={n} T={T} params={n_params} {p_dt} calls (add, param, derived, chain) "
+          f"{calls}")
+    w0 = [1 + 0.02 * _tensor(rng, (n,), torch.float32) for _ in range(n_params)]
+    x0 = _tensor(rng, (T, n), torch.bfloat16)
+    r0 = _tensor(rng, (T, n), torch.float32, 2.0)
+    proj = [_tensor(rng, (T, n), torch.float32) for _ in calls]
+
+    def run(defer, separate=False):
+        old = nr.DEFER_WEIGHT_GRAD
+        nr.DEFER_WEIGHT_GRAD = defer
+        try:
+            ps = [torch.nn.Parameter(w.to(p_dt)) for w in w0]
+            x, r = x0.clone().requires_grad_(), r0.clone().requires_grad_()
+            h, res, loss, uses = x, r, 0.0, []
+            for (add, pi, derived, chain), pj in zip(calls, proj):
+                base = ps[pi] * 1.0 if separate else ps[pi]  # a tensor of its own per use
+                uses.append((pi, base))
+                w = base * 0.5 if derived else base
+                inp = h if chain else x
+                if add:
+                    res, y = nr.add_rmsnorm(res, inp, w, EPS, torch.bfloat16)
+                else:
+                    y = nr.rmsnorm(inp, w, EPS)
+                h = y.to(torch.bfloat16)
+                loss = loss + (y.float() * pj).sum()
+            if separate:
+                return uses, torch.autograd.grad(loss, [b for _, b in uses])
+            loss.backward()
+            torch.cuda.synchronize()
+            return [p.grad for p in ps], x.grad, r.grad
+        finally:
+            nr.DEFER_WEIGHT_GRAD = old
+
+    gd, xd, rd = run(True)
+    gp, xp, rp = run(False)
+    uses, contrib = run(False, separate=True)
+    eps = {torch.float32: 2.0 ** -23, torch.bfloat16: 2.0 ** -8}[p_dt]
+    for i, (a, b) in enumerate(zip(gd, gp)):
+        mine = [c.float() for (pi, _), c in zip(uses, contrib) if pi == i]
+        assert (a is None) == (b is None) == (not mine)
+        if a is None:
+            continue
+        assert a.dtype == p_dt
+        if len(mine) == 1:
+            assert torch.equal(a, b)
+        else:
+            bound = len(mine) * eps * torch.stack(mine).abs().sum(0)
+            assert torch.all((a.float() - b.float()).abs() <= bound), \
+                ((a.float() - b.float()).abs() - bound).max().item()
+    for a, b in ((xd, xp), (rd, rp)):
+        assert (a is None) == (b is None)
+        if a is not None:
+            assert torch.equal(a, b)
+
+
 def _lengths(rng, n_seq, hi, p_empty=0.15):
     lens = [0 if rng.random() < p_empty else int(rng.integers(1, hi)) for _ in range(n_seq)]
     if max(lens) == 0:
