@@ -60,8 +60,16 @@ def _norm_case(seed):
 def test_random_rmsnorm(seed):
     nr = _nr()
     rng, rows, n, dtype, recompute = _norm_case(seed)
-    print(f"seed {seed}: rows={rows} n={n} {dtype} recompute_rstd={recompute}")
-    x = _tensor(rng, (rows, n), dtype).requires_grad_()
+    # half the cases read x as a column slice of a wider buffer: a row stride above n, and an
+    # offset that may leave the rows without 16-byte alignment (the element-wise kernels)
+    pad, off = (int(rng.integers(0, 40)), int(rng.integers(0, 9))) if rng.integers(2) else (0, 0)
+    print(f"seed {seed}: rows={rows} n={n} {dtype} recompute_rstd={recompute} "
+          f"row pad={pad} offset={off}")
+    if pad or off:
+        buf = _tensor(rng, (rows, n + pad + off), dtype).requires_grad_()
+        x = buf[:, off:off + n]
+    else:
+        x = _tensor(rng, (rows, n), dtype).requires_grad_()
     w = (1 + 0.02 * _tensor(rng, (n,), torch.float32)).requires_grad_()
     dy = _tensor(rng, (rows, n), dtype)
     y = nr.rmsnorm(x, w, EPS, recompute_rstd=recompute)
