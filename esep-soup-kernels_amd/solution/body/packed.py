@@ -449,7 +449,9 @@ class _RecomputeMLP(torch.autograd.Function):
 
     apply(x_gate, x_up, r, w_norm, eps, gate, up, down). Saved: x itself, or (when the norm
     that produced x did not keep its output) the norm's fp32 input r and weight, x then being
-    recomputed bit-exactly by the same norm kernel in backward. Forward: g, u from the two
+    recomputed bit-exactly by the same norm kernel in backward; for nn.Linear also the three
+    weights in the dtype the projections compute in (the casts HF's autograd holds as well;
+    casting again in backward cost five weight casts per layer). Forward: g, u from the two
     projections (NF4: nf4.linear4bit, dequant on the HIP kernel + fp16 GEMM), h = silu(g) * u on
     the HIP kernel (into g), out from the down projection. Backward: dh = dout W_down, g and u
     recomputed, (dg, du) by the HIP kernel in place. NF4: W_down from one dequant launch, W_gate
@@ -473,16 +475,23 @@ class _RecomputeMLP(torch.autograd.Function):
             u = nf4.linear4bit(x2, up, keep_fp16=True).contiguous()
             _hip.swiglu_fwd(h, u, h)
             out = nf4.linear4bit(h, down, keep_fp16=True)
+            weights = ()
         else:
-            h = F.linear(x2, gate.weight).contiguous()
-            u = F.linear(x2, up.weight).contiguous()
+            # The weights in the dtype the projections compute in, cast once and kept for the
+            # backward (the bits autocast's own cast gives): autocast caches casts only of
+            # leaves that require grad, so frozen fp32 weights would be cast again at each of
+            # their five uses in backward. Weights already in that dtype are kept as they are.
+            dt = torch.get_autocast_dtype("cuda") if torch.is_autocast_enabled("cuda") else None
+            weights = tuple(lin.weight if dt is None else lin.weight.to(dt)
+                            for lin in (gate, up, down))
+            h = F.linear(x2, weights[0]).contiguous()
+            u = F.linear(x2, weights[1]).contiguous()
             _hip.swiglu_fwd(h, u, h)
-            out = F.linear(h, down.weight)
+            out = F.linear(h, weights[2])
         del h, u
-        if r is None:
-            ctx.save_for_backward(x2)
-        else:
-            ctx.save_for_backward(r, w_norm)
+        saved = (x2,) if r is None else (r, w_norm)
+        ctx.n_x = len(saved)
+        ctx.save_for_backward(*saved, *weights)
         ctx.from_residual, ctx.eps = r is not None, eps
         ctx.shape, ctx.x_dtype, ctx.proj = shape, x.dtype, (gate, up, down)
         return out.view(*shape[:-1], out.shape[-1])
@@ -493,13 +502,16 @@ class _RecomputeMLP(torch.autograd.Function):
         from . import _hip
 
         gate, up, down = ctx.proj
+        saved = ctx.saved_tensors
         if ctx.from_residual:
             from .norm_rope import rmsnorm_recompute
 
-            r, w_norm = ctx.saved_tensors
+            r, w_norm = saved[:2]
             x2 = rmsnorm_recompute(r.reshape(-1, r.shape[-1]), w_norm, ctx.eps, ctx.x_dtype)
         else:
-            (x2,) = ctx.saved_tensors
+            x2 = saved[0]
+        weights = saved[ctx.n_x:]
+        del saved
         dout2 = dout.reshape(-1, dout.shape[-1])
         if ctx.nf4:
             nf4 = _nf4()
@@ -517,15 +529,16 @@ class _RecomputeMLP(torch.autograd.Function):
             dx = torch.mm(g, w_gate)
             dx.addmm_(u, w_up)
             return dx.view(ctx.shape), None, None, None, None, None, None, None
-        dh = torch.matmul(dout2, down.weight)
-        g = F.linear(x2, gate.weight).contiguous()
-        u = F.linear(x2, up.weight).contiguous()
+        w_gate, w_up, w_down = weights
+        dh = torch.matmul(dout2, w_down)
+        g = F.linear(x2, w_gate).contiguous()
+        u = F.linear(x2, w_up).contiguous()
         del x2
         _hip.swiglu_bwd(dh.to(g.dtype).contiguous(), g, u, g, u)  # dg into g, du into u
         del dh
-        dx_gate = torch.matmul(g, gate.weight).to(ctx.x_dtype)
+        dx_gate = torch.matmul(g, w_gate).to(ctx.x_dtype)
         del g
-        dx_up = torch.matmul(u, up.weight).to(ctx.x_dtype)
+        dx_up = torch.matmul(u, w_up).to(ctx.x_dtype)
         return dx_gate.view(ctx.shape), dx_up.view(ctx.shape), None, None, None, None, None, None
 
 

@@ -19,6 +19,8 @@ installed in this build's environment, where a module whose class is named Linea
 attributes is taken as one (is_linear4bit), and patch() has no class to patch.
 """
 
+import functools
+
 import torch
 
 from ..body import _hip
@@ -155,8 +157,11 @@ _FP16, _FP32 = torch.float16, torch.float32
 _orig_forward = None  # Linear4bit.forward as it was before patch()
 
 
+@functools.cache
 def _bnb_class():
-    """bitsandbytes.nn.Linear4bit, or None where bitsandbytes is not installed."""
+    """bitsandbytes.nn.Linear4bit, or None where bitsandbytes is not installed. Looked up once
+    per process: Python does not remember a failed import, so without bitsandbytes every
+    lookup would search sys.path again (the packed decoder asks ten times per layer)."""
     try:
         from bitsandbytes.nn import Linear4bit
     except Exception:

@@ -108,7 +108,7 @@ def test_recompute_mlp_matches_and_saves_no_intermediate(dtype):
     saved = []
 
     def pack(t):
-        saved.append(tuple(t.shape))
+        saved.append((tuple(t.shape), t.data_ptr()))
         return t
 
     assert packed._mlp_layers(mlp, x) is not None
@@ -118,10 +118,68 @@ def test_recompute_mlp_matches_and_saves_no_intermediate(dtype):
     tol = dict(atol=2e-3, rtol=1e-2) if dtype == torch.float16 else dict(atol=2e-2, rtol=2e-2)
     torch.testing.assert_close(got, want, **tol)
     torch.testing.assert_close(dx, dx_want, **tol)
-    assert saved and all(I not in shp for shp in saved), saved
+    # nothing [T, I] saved; the only I-sized tensors kept are the weights themselves (already
+    # in the compute dtype, so kept without a copy)
+    weights = {p.data_ptr() for p in mlp.parameters()}
+    assert saved and all(T not in shp for shp, ptr in saved if I in shp), saved
+    assert all(ptr in weights for shp, ptr in saved if I in shp), saved
     # a trainable projection sends the block to the non-recompute path
     mlp.up_proj.weight.requires_grad_(True)
     assert packed._mlp_layers(mlp, x) is None
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+def test_recompute_mlp_autocast_casts_each_weight_once(dtype):
+    """fp32 frozen weights under autocast (a LoRA run's fp32 master copy): the recompute MLP
+    matches HF's Qwen2MLP under the same autocast, its forward casts each of the three weights
+    once, and its backward (g and u recomputed, dh and dx products) casts none: it uses the
+    forward's casts. Autocast caches only casts of leaves that require grad, so reading the
+    frozen weights again in backward would cast them five more times."""
+    from torch.utils._python_dispatch import TorchDispatchMode
+    from transformers import Qwen2Config
+    from transformers.models.qwen2 import modeling_qwen2
+
+    from solution.body import packed
+
+    T, H, I = 200, 128, 352
+    mlp = modeling_qwen2.Qwen2MLP(Qwen2Config(hidden_size=H, intermediate_size=I)).to(DEV)
+    for prm in mlp.parameters():
+        prm.requires_grad_(False)
+    g_ = gen(10)
+    x = torch.randn(1, T, H, generator=g_).to(dtype).to(DEV).requires_grad_()
+    dout = torch.randn(1, T, H, generator=g_).to(dtype).to(DEV)
+
+    class Casts(TorchDispatchMode):
+        """Records casts of [I, H] / [H, I] fp32 tensors (the weights) and counts products."""
+
+        def __init__(self):
+            super().__init__()
+            self.casts, self.products = [], 0
+
+        def __torch_dispatch__(self, func, types, args=(), kwargs=None):
+            a = args[0] if args else None
+            if (func == torch.ops.aten._to_copy.default and a.dtype == torch.float32
+                    and I in a.shape and a.dim() == 2):
+                self.casts.append(tuple(a.shape))
+            if func in (torch.ops.aten.mm.default, torch.ops.aten.addmm.default):
+                self.products += 1
+            return func(*args, **(kwargs or {}))
+
+    with torch.autocast("cuda", dtype=dtype):
+        want = mlp(x)
+        assert packed._mlp_layers(mlp, x) is not None
+        fwd = Casts()
+        with fwd:
+            got = packed._mlp(mlp, (x, x))
+    (dx_want,) = torch.autograd.grad(want, [x], dout)
+    bwd = Casts()
+    with bwd:
+        (dx,) = torch.autograd.grad(got, [x], dout)
+    assert sorted(fwd.casts) == sorted([(I, H), (I, H), (H, I)]), fwd.casts
+    assert bwd.products >= 5 and bwd.casts == [], (bwd.products, bwd.casts)  # 3 recomputed + 2 dx
+    tol = dict(atol=2e-3, rtol=1e-2) if dtype == torch.float16 else dict(atol=2e-2, rtol=2e-2)
+    torch.testing.assert_close(got, want, **tol)
+    torch.testing.assert_close(dx, dx_want, **tol)
 
 
 def test_swiglu_bench_shape():
