@@ -1220,6 +1220,9 @@ def main():
     ap.add_argument("--no-lm-head", action="store_true", help="skip the fused LM head measurement")
     ap.add_argument("--no-packed", action="store_true",
                     help="skip the end-to-end packed decoder against HF's original forward")
+    ap.add_argument("--packed-only", action="store_true",
+                    help="profiling run: only the end-to-end packed decoder leg (its log line, "
+                         "no JSON)")
     ap.add_argument("--pmc-kernel", choices=["rmsnorm_fwd", "rmsnorm_bwd", "rope_fwd", "rope_bwd"],
                     help="counter-collection run: a calibration copy of 256 MiB (read 256 MiB, "
                          "write 256 MiB) three times, then one launch per layer of this kernel "
@@ -1238,6 +1241,9 @@ def main():
     _hip.lib()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
+    if args.packed_only:
+        run_packed_decoder(dev, 5)
+        return 0
     cfg = CFG4
     save_rstd = args.rstd == "saved"
     log(f"allocating config 4 ({cfg['layers']} layers, T={cfg['B'] * cfg['S']}) on {torch.cuda.get_device_name(dev)}")
