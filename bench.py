@@ -29,6 +29,8 @@ the CPU baseline: the PyTorch-eager fp32 restatement of HF's Qwen2RMSNorm / rota
 (oracle/hf_eager.py) timed on this host's cores on one layer of the same workload.
 
     python bench.py [--steps K] [--warmup W] [--rstd saved|recomputed] [--no-cpu]
+    python bench.py --pmc-kernel rmsnorm_bwd   # counter run for rocprofv3 --pmc (no timing)
+    python bench.py --packed-only              # the end-to-end packed decoder leg alone
 """
 
 import argparse
