@@ -989,29 +989,34 @@ def run_packed_decoder(dev, reps, layers=28):
         out.float().square().mean().backward()
 
     def timed():
+        """ms per step, and the step's peak device memory above what was allocated before it
+        (weights, their gradients and the inputs), in GB."""
         for _ in range(2):
             step()
         torch.cuda.synchronize()
+        base = torch.cuda.memory_allocated(dev)
+        torch.cuda.reset_peak_memory_stats(dev)
         e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
         e0.record()
         for _ in range(reps):
             step()
         e1.record()
         torch.cuda.synchronize()
-        return e0.elapsed_time(e1) / reps
+        return e0.elapsed_time(e1) / reps, (torch.cuda.max_memory_allocated(dev) - base) / 1e9
 
     with _hip.count_launches() as names:
         step()
         torch.cuda.synchronize()
-    ours = timed()
+    ours, ours_gb = timed()
     cls = modeling_qwen2.Qwen2Model
     patched = cls.forward
     cls.forward = patched.__wrapped__
     try:
-        hf = timed()
+        hf, hf_gb = timed()
     finally:
         cls.forward = patched
-    log(f"packed decoder ({layers} layers): {ours:.2f} ms vs HF's original forward {hf:.2f} ms")
+    log(f"packed decoder ({layers} layers): {ours:.2f} ms vs HF's original forward {hf:.2f} ms; "
+        f"step peak memory {ours_gb:.2f} vs {hf_gb:.2f} GB")
     del model
     torch.cuda.empty_cache()
     return {"workload": f"Qwen2.5-1.5B-shaped Qwen2Model, {layers} layers, random weights, fp32 master "
@@ -1020,6 +1025,9 @@ def run_packed_decoder(dev, reps, layers=28):
                         "packed forward against HF's original forward (sdpa) on the same GPU",
             "layers": layers, "tokens": int(lens.sum()), "padded_tokens": 8 * 1024,
             "ours_ms": round(ours, 3), "hf_original_ms": round(hf, 3), "speedup": round(hf / ours, 2),
+            "step_peak_GB": {"ours": round(ours_gb, 3), "hf_original": round(hf_gb, 3),
+                             "what": "peak device memory of the timed steps above what was "
+                                     "allocated before them (weights, gradients, inputs)"},
             "hip_launches_per_step": len(names), "kernels": sorted(set(names))}
 
 
