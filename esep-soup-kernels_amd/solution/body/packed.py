@@ -45,11 +45,13 @@ log = logging.getLogger(__name__)
 # (packed.py:106) turns every HIP piece off (the packed layout on torch ops);
 # NORM_SAVE_OUTPUT (:149) makes the decoder-layer norms save their 16-bit output instead of
 # the fp32 residual; USE_LORA_KERNELS (:186) runs LoRA projections as modules when off;
-# RECOMPUTE_MLP (:448) sends frozen MLPs through _RecomputeMLP.
+# RECOMPUTE_MLP (:448) sends frozen MLPs through _RecomputeMLP. FUSE_QKV (this build's) runs
+# plain nn.Linear q / k / v bases as one GEMM against their concatenated weights (_qkv).
 USE_KERNELS = True
 NORM_SAVE_OUTPUT = True
 USE_LORA_KERNELS = True
 RECOMPUTE_MLP = True
+FUSE_QKV = True
 
 _KERNEL_FLOATS = (torch.float16, torch.bfloat16, torch.float32)
 
@@ -276,26 +278,68 @@ def _project_q(module, x, x_lora=None):
     return q.view(1, x2.shape[0], -1), term.view(1, x2.shape[0], -1)
 
 
+def _qkv_route(module, x):
+    """_lora_route's answer for one of q / k / v, except that a plain nn.Linear without hooks
+    (which _lora_route leaves to module(x)) is (module, None) when FUSE_QKV is on."""
+    route = _lora_route(module, x)
+    if (route is None and FUSE_QKV and USE_KERNELS and type(module) is torch.nn.Linear
+            and not _has_hooks(module)):
+        return module, None
+    return route
+
+
+def _linear_multi(x2, bases):
+    """Outputs of plain nn.Linear layers that read the same 2-D x2, as column views of ONE GEMM
+    against their concatenated weights and biases, or None when they differ in weight dtype,
+    device, input width or bias presence, or would not compute in x2's dtype (autocast to it,
+    or weights of it). Under autocast the concatenation is cast once (the bits of autocast's
+    per-weight casts). Autograd reaches each weight through the cast and the concatenation
+    (one dW GEMM for all trainable ones, sliced by the cat's backward), and the split's
+    backward gathers the output gradients for one dX GEMM."""
+    ws = [b.weight for b in bases]
+    bs = [b.bias for b in bases]
+    if (len({(w.dtype, w.device, w.dim(), w.shape[-1]) for w in ws}) != 1 or ws[0].dim() != 2
+            or (any(b is None for b in bs) and not all(b is None for b in bs))):
+        return _fallback("fused q/k/v", "projections differ in weight dtype, shape or bias")
+    if torch.is_autocast_enabled("cuda"):
+        dt = torch.get_autocast_dtype("cuda")
+    else:
+        dt = ws[0].dtype
+    if dt != x2.dtype:
+        return _fallback("fused q/k/v", f"x {x2.dtype} against compute dtype {dt}")
+    w = torch.cat(ws).to(dt)
+    b = None if bs[0] is None else torch.cat(bs).to(dt)
+    y = F.linear(x2, w, b)
+    return y.split([t.shape[0] for t in ws], dim=-1)
+
+
 def _qkv(attn, x_q, x_ql, x_vl):
     """(q, q term, k, v) as _project_q / _project give them, with the three base projections as
-    ONE nf4.linear4bit_multi call on x_q (one dequant launch into W_cat, one GEMM; backward one
-    re-dequant and one dX GEMM) when q, k and v all take this path onto NF4 bases, k without a
-    LoRA term of its own; else None (the separate calls run). q, k, v are column views of the
-    one output; v's LoRA term is added out of place (v is a view). The norm backward then gets
-    one base gradient (through x_q) beside the q and v LoRA gradients (x_ql, x_vl); the k and v
-    base copies of the norm output get none (reference packed.py:321-352)."""
-    routes = [_lora_route(m, x_q) for m in (attn.q_proj, attn.k_proj, attn.v_proj)]
+    ONE GEMM on x_q when q, k and v all take this path, k without a LoRA term of its own: NF4
+    bases through nf4.linear4bit_multi (one dequant launch into W_cat, one GEMM; backward one
+    re-dequant and one dX GEMM; reference packed.py:321-352), plain nn.Linear bases (or plain
+    layers themselves, FUSE_QKV) through _linear_multi. Else None (the separate calls run).
+    q, k, v are column views of the one output; v's LoRA term is added out of place (v is a
+    view). The norm backward then gets one base gradient (through x_q) beside the q and v LoRA
+    gradients (x_ql, x_vl); the k and v base copies of the norm output get none."""
+    routes = [_qkv_route(m, x_q) for m in (attn.q_proj, attn.k_proj, attn.v_proj)]
     if any(r is None for r in routes) or routes[1][1] is not None:
         return None
     nf4 = _nf4()
     bases = [r[0] for r in routes]
-    if not all(nf4.is_linear4bit(b) for b in bases):
+    x2 = x_q.reshape(-1, x_q.shape[-1])
+    n_tok = x2.shape[0]
+    if all(nf4.is_linear4bit(b) for b in bases):
+        q, k, v = nf4.linear4bit_multi(x2, bases)
+    elif FUSE_QKV and all(type(b) is torch.nn.Linear for b in bases):
+        qkv = _linear_multi(x2, bases)
+        if qkv is None:
+            return None
+        q, k, v = qkv
+    else:
         return None
     from .lora import LoRADeltaFunction, LoRAFunction
 
-    x2 = x_q.reshape(-1, x_q.shape[-1])
-    n_tok = x2.shape[0]
-    q, k, v = nf4.linear4bit_multi(x2, bases)
     q_term = None
     if routes[0][1] is not None:
         q_term = LoRADeltaFunction.apply(x_ql.reshape(-1, x_ql.shape[-1]), *routes[0][1])

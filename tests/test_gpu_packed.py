@@ -242,3 +242,43 @@ def test_packed_recompute_mlp(save_output, monkeypatch):
     monkeypatch.setattr(packed, "RECOMPUTE_MLP", False)
     off = _run(model, ids, mask, labels)
     _compare(ref, off, mask)
+
+
+@pytest.mark.parametrize("variant", ["plain", "frozen"])
+@pytest.mark.parametrize("dtype", [torch.float16, torch.bfloat16], ids=["fp16", "bf16"])
+def test_fused_qkv(variant, dtype, monkeypatch):
+    """Plain nn.Linear q / k / v run as one GEMM against their concatenated weights (FUSE_QKV):
+    one fused call per layer and forward, against HF's original forward at the usual
+    tolerances and against the three separate projections (FUSE_QKV off) at the same ones;
+    the trainable q / v weights get their gradients through the concatenation (k's is
+    never formed: frozen), and the norm's k and v copies get none."""
+    from solution.body import packed, patch
+
+    patch()
+    model = _build(variant)
+    ids, mask, labels = _batch()
+    with _original_forward():
+        ref = _run(model, ids, mask, labels, dtype=dtype)
+    calls = []
+    orig = packed._linear_multi
+
+    def counting(x2, bases):
+        out = orig(x2, bases)
+        calls.append(out is not None)
+        return out
+
+    monkeypatch.setattr(packed, "_linear_multi", counting)
+    fused = _run(model, ids, mask, labels, dtype=dtype)
+    n_layers = model.config.num_hidden_layers
+    assert calls == [True] * (2 * n_layers), calls  # loss forward + hidden forward
+    monkeypatch.setattr(packed, "FUSE_QKV", False)
+    calls.clear()
+    separate = _run(model, ids, mask, labels, dtype=dtype)
+    assert calls == []
+    tol = dict(tol_h=5e-3, tol_loss=1e-3, tol_g=2e-2) if dtype == torch.float16 else \
+        dict(tol_h=3e-2, tol_loss=5e-3, tol_g=6e-2)
+    _compare(ref, fused, mask, **tol)
+    _compare(separate, fused, mask, **tol)
+    if variant == "frozen":
+        assert set(fused["grads"]) == {n for n, p in model.named_parameters() if p.requires_grad}
+        assert all("k_proj" not in n for n in fused["grads"])
