@@ -22,7 +22,9 @@ Per decoder layer, each piece has a guard and an HF / torch fallback (warned onc
               RoPE kernel as q_delta (reference packed.py:240-352). NF4 base layers
               (bitsandbytes' Linear4bit interface, solution.nf4) run through nf4.linear4bit on
               the HIP dequant, and q/k/v on NF4 bases as one nf4.linear4bit_multi call (one
-              dequant launch and one GEMM) on the input norm's output (reference :184-352).
+              dequant launch and one GEMM) on the input norm's output (reference :184-352);
+              q/k/v on plain nn.Linear bases likewise as one GEMM against their concatenated
+              weights (FUSE_QKV; the reference runs those three apart).
   RoPE        norm_rope.rope on the packed positions with the model's inv_freq.
   attention   attention.varlen_attention over all rows in one launch per direction; else a
               per-row SDPA loop (reference packed.py:404-436).
@@ -346,6 +348,11 @@ def _qkv(attn, x_q, x_ql, x_vl):
         q_term = q_term.view(1, n_tok, -1)
     if routes[2][1] is not None:
         v = LoRAFunction.apply(x_vl.reshape(-1, x_vl.shape[-1]), v, *routes[2][1])
+    else:
+        # v as a view would keep the whole fused output (q's and k's columns too; RoPE writes
+        # new tensors) alive until the attention backward: 21 MB per layer at the Qwen2.5-1.5B
+        # shape, against a copy of v's 3 MB
+        v = v.contiguous()
     return q.view(1, n_tok, -1), q_term, k.view(1, n_tok, -1), v.view(1, n_tok, -1)
 
 
