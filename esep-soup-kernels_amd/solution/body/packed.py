@@ -291,13 +291,13 @@ def _qkv_route(module, x):
 
 
 def _linear_multi(x2, bases):
-    """Outputs of plain nn.Linear layers that read the same 2-D x2, as column views of ONE GEMM
-    against their concatenated weights and biases, or None when they differ in weight dtype,
-    device, input width or bias presence, or would not compute in x2's dtype (autocast to it,
-    or weights of it). Under autocast the concatenation is cast once (the bits of autocast's
-    per-weight casts). Autograd reaches each weight through the cast and the concatenation
-    (one dW GEMM for all trainable ones, sliced by the cat's backward), and the split's
-    backward gathers the output gradients for one dX GEMM."""
+    """The outputs of plain nn.Linear layers that read the same 2-D x2, side by side in the
+    columns of ONE GEMM's output against their concatenated weights and biases, or None when
+    they differ in weight dtype, device, input width or bias presence, or would not compute in
+    x2's dtype (autocast to it, or weights of it). Under autocast the concatenation is cast
+    once (the bits of autocast's per-weight casts). Autograd reaches each weight through the
+    cast and the concatenation (one dW GEMM for all trainable ones, sliced by the cat's
+    backward), and one dX GEMM reads the output's whole gradient."""
     ws = [b.weight for b in bases]
     bs = [b.bias for b in bases]
     if (len({(w.dtype, w.device, w.dim(), w.shape[-1]) for w in ws}) != 1 or ws[0].dim() != 2
@@ -311,18 +311,77 @@ def _linear_multi(x2, bases):
         return _fallback("fused q/k/v", f"x {x2.dtype} against compute dtype {dt}")
     w = torch.cat(ws).to(dt)
     b = None if bs[0] is None else torch.cat(bs).to(dt)
-    y = F.linear(x2, w, b)
-    return y.split([t.shape[0] for t in ws], dim=-1)
+    return F.linear(x2, w, b)
 
 
-def _qkv(attn, x_q, x_ql, x_vl):
-    """(q, q term, k, v) as _project_q / _project give them, with the three base projections as
-    ONE GEMM on x_q when q, k and v all take this path, k without a LoRA term of its own: NF4
-    bases through nf4.linear4bit_multi (one dequant launch into W_cat, one GEMM; backward one
-    re-dequant and one dX GEMM; reference packed.py:321-352), plain nn.Linear bases (or plain
-    layers themselves, FUSE_QKV) through _linear_multi. Else None (the separate calls run).
-    q, k, v are column views of the one output; v's LoRA term is added out of place (v is a
-    view). The norm backward then gets one base gradient (through x_q) beside the q and v LoRA
+def _rope_kernel_ok(rope_in, q, q_delta):
+    """The RoPE kernel takes q (and a k of q's dtype) with these rotary inputs."""
+    return (rope_in.positions is not None and q.dtype in _KERNEL_FLOATS and q.is_cuda
+            and (q_delta is None or q_delta.dtype == q.dtype))
+
+
+class _QKVRope(torch.autograd.Function):
+    """RoPE on the q and k columns of the fused q / k / v output y [T, nq + nk + nv], and v
+    copied out of it: apply(y, nq, nk, head_dim, positions [T], inv_freq, q_delta [T, nq] or
+    None) -> (q rotated [1, T, nq / D, D], k rotated [1, T, nk / D, D], v [T, nv]), q_delta
+    added to q inside the kernel before the rotation. The backward writes the inverse
+    rotations of dq and dk and a copy of dv straight into the columns of one gradient of y,
+    which the fused GEMM's backward reads whole; with column views of y instead, the split's
+    backward concatenates three separate gradients (a copy of all of them: 19 us per layer at
+    the Qwen2.5-1.5B shape against a copy of v's columns). q_delta gets the gradient of q's
+    columns, as Rope gives it. v is a copy so that y is freed once RoPE has read it."""
+
+    @staticmethod
+    def forward(ctx, y, nq, nk, head_dim, positions, inv_freq, q_delta):
+        from . import _hip
+
+        T = y.shape[0]
+        q4 = y[:, :nq].view(1, T, nq // head_dim, head_dim)
+        k4 = y[:, nq:nq + nk].view(1, T, nk // head_dim, head_dim)
+        qd4 = None if q_delta is None else q_delta.reshape(q4.shape)
+        qo = torch.empty(q4.shape, device=y.device, dtype=y.dtype)
+        ko = torch.empty(k4.shape, device=y.device, dtype=y.dtype)
+        pos2 = positions.view(1, -1)
+        if T > 0:
+            _hip.rope(q4, k4, qo, ko, inv_freq, 1.0, q_delta=qd4, positions=pos2)
+        v = y[:, nq + nk:].contiguous()
+        ctx.save_for_backward(positions, inv_freq)
+        ctx.dims, ctx.dtype = (T, nq, nk, y.shape[1], head_dim), y.dtype
+        ctx.has_qd = q_delta is not None
+        return qo, ko, v
+
+    @staticmethod
+    def backward(ctx, dqo, dko, dv):
+        from . import _hip
+
+        positions, inv_freq = ctx.saved_tensors
+        T, nq, nk, n, head_dim = ctx.dims
+        dy = torch.empty((T, n), device=inv_freq.device, dtype=ctx.dtype)
+        dq4 = dy[:, :nq].view(1, T, nq // head_dim, head_dim)
+        dk4 = dy[:, nq:nq + nk].view(1, T, nk // head_dim, head_dim)
+        # an unused output's gradient is zero (as in Rope)
+        dqo = torch.zeros_like(dq4) if dqo is None else dqo.contiguous()
+        dko = torch.zeros_like(dk4) if dko is None else dko.contiguous()
+        if T > 0:
+            _hip.rope(dqo, dko, dq4, dk4, inv_freq, -1.0, positions=positions.view(1, -1))
+        if dv is None:
+            dy[:, nq + nk:].zero_()
+        else:
+            dy[:, nq + nk:].copy_(dv)
+        dqd = dy[:, :nq] if ctx.has_qd and ctx.needs_input_grad[6] else None
+        return dy, None, None, None, None, None, dqd
+
+
+def _qkv(attn, x_q, x_ql, x_vl, rope_in):
+    """(q, q term, k, v, rotated) as _project_q / _project give them, with the three base
+    projections as ONE GEMM on x_q when q, k and v all take this path, k without a LoRA term of
+    its own: NF4 bases through nf4.linear4bit_multi (one dequant launch into W_cat, one GEMM;
+    backward one re-dequant and one dX GEMM; reference packed.py:321-352), plain nn.Linear
+    bases (or plain layers themselves, FUSE_QKV) through _linear_multi. Else None (the separate
+    calls run). The fused plain output goes through _QKVRope when the RoPE kernel takes it
+    (rotated True: q and k come back rotated, q's LoRA term added inside); otherwise q, k, v
+    are column views of the one output (rotated False). v's LoRA term is added out of place.
+    The norm backward then gets one base gradient (through x_q) beside the q and v LoRA
     gradients (x_ql, x_vl); the k and v base copies of the norm output get none."""
     routes = [_qkv_route(m, x_q) for m in (attn.q_proj, attn.k_proj, attn.v_proj)]
     if any(r is None for r in routes) or routes[1][1] is not None:
@@ -331,13 +390,14 @@ def _qkv(attn, x_q, x_ql, x_vl):
     bases = [r[0] for r in routes]
     x2 = x_q.reshape(-1, x_q.shape[-1])
     n_tok = x2.shape[0]
+    y = None
     if all(nf4.is_linear4bit(b) for b in bases):
         q, k, v = nf4.linear4bit_multi(x2, bases)
     elif FUSE_QKV and all(type(b) is torch.nn.Linear for b in bases):
-        qkv = _linear_multi(x2, bases)
-        if qkv is None:
+        y = _linear_multi(x2, bases)
+        if y is None:
             return None
-        q, k, v = qkv
+        sizes = [b.weight.shape[0] for b in bases]
     else:
         return None
     from .lora import LoRADeltaFunction, LoRAFunction
@@ -345,15 +405,25 @@ def _qkv(attn, x_q, x_ql, x_vl):
     q_term = None
     if routes[0][1] is not None:
         q_term = LoRADeltaFunction.apply(x_ql.reshape(-1, x_ql.shape[-1]), *routes[0][1])
+    rotated = y is not None and _rope_kernel_ok(rope_in, y, q_term)
+    if rotated:
+        q, k, v = _QKVRope.apply(y, sizes[0], sizes[1], attn.head_dim, rope_in.positions,
+                                 rope_in.inv_freq, q_term)
+        q_term = None  # added inside the kernel
+    elif y is not None:
+        q, k, v = y.split(sizes, dim=-1)
+    if q_term is not None:
         q_term = q_term.view(1, n_tok, -1)
     if routes[2][1] is not None:
         v = LoRAFunction.apply(x_vl.reshape(-1, x_vl.shape[-1]), v, *routes[2][1])
-    else:
+    elif not rotated:
         # v as a view would keep the whole fused output (q's and k's columns too; RoPE writes
         # new tensors) alive until the attention backward: 21 MB per layer at the Qwen2.5-1.5B
         # shape, against a copy of v's 3 MB
         v = v.contiguous()
-    return q.view(1, n_tok, -1), q_term, k.view(1, n_tok, -1), v.view(1, n_tok, -1)
+    if rotated:
+        return q, None, k, v.view(1, n_tok, -1), True
+    return q.view(1, n_tok, -1), q_term, k.view(1, n_tok, -1), v.view(1, n_tok, -1), False
 
 
 # ----------------------------------------------------------------------------------------
@@ -392,9 +462,7 @@ def _rope(q, k, rope_in, q_delta=None):
     """Rotated (q + q_delta, k) for q [1, T, Hq, D], k [1, T, Hk, D] (reference
     packed.py:382-401): on the kernel when it takes these inputs (the add happens inside it,
     in q's dtype), else HF's apply_rotary_pos_emb after the add."""
-    kernel_ok = (rope_in.positions is not None and q.dtype in _KERNEL_FLOATS and q.is_cuda
-                 and k.dtype == q.dtype and (q_delta is None or q_delta.dtype == q.dtype))
-    if kernel_ok:
+    if _rope_kernel_ok(rope_in, q, q_delta) and k.dtype == q.dtype:
         from .norm_rope import rope
 
         # squeeze, not indexing: its backward is a view too
@@ -630,14 +698,17 @@ def _layer(layer, residual, delta, rope_in, lens):
     residual, (x_q, x_ql, x_k, x_v, x_vl) = _add_norm(layer.input_layernorm, residual, delta,
                                                       n_out=5, save_output=NORM_SAVE_OUTPUT)
     n_tok, head_dim = x_q.shape[1], attn.head_dim
-    fused = _qkv(attn, x_q, x_ql, x_vl)
+    fused = _qkv(attn, x_q, x_ql, x_vl, rope_in)
+    rotated = False
     if fused is not None:
-        q, q_term, k, v = fused
+        q, q_term, k, v, rotated = fused
     else:
         q, q_term = _project_q(attn.q_proj, x_q, x_ql)
         k = _project(attn.k_proj, x_k)
         v = _project(attn.v_proj, x_v, x_vl)
-    q, k = _rope(q.view(1, n_tok, -1, head_dim), k.view(1, n_tok, -1, head_dim), rope_in, q_term)
+    if not rotated:
+        q, k = _rope(q.view(1, n_tok, -1, head_dim), k.view(1, n_tok, -1, head_dim), rope_in,
+                     q_term)
     o = _project(attn.o_proj, _attention(attn, q, k, v.view(1, n_tok, -1, head_dim), lens))
     post = layer.post_attention_layernorm
     residual, xs, eps = _add_norm(post, residual, o, with_eps=True, n_out=2,

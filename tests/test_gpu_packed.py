@@ -282,3 +282,43 @@ def test_fused_qkv(variant, dtype, monkeypatch):
     if variant == "frozen":
         assert set(fused["grads"]) == {n for n, p in model.named_parameters() if p.requires_grad}
         assert all("k_proj" not in n for n in fused["grads"])
+
+
+@pytest.mark.parametrize("with_delta", [False, True], ids=["no_delta", "q_delta"])
+@pytest.mark.parametrize("v_grad", [True, False], ids=["dv", "no_dv"])
+def test_qkv_rope_matches_split(with_delta, v_grad):
+    """_QKVRope (RoPE on the fused q / k / v output's columns, the backward writing the
+    gradient of all three column blocks into one tensor) against the column views it replaces:
+    y.split, norm_rope.rope on the q / k views (q_delta added inside) and a copy of v. The same
+    kernels on the same data: outputs and gradients (y's, q_delta's) bit for bit, with and
+    without v's gradient (its columns zero)."""
+    from solution.body import packed
+    from solution.body.norm_rope import default_inv_freq, rope
+
+    T, HQ, HK, D = 301, 4, 2, 64
+    nq, nk = HQ * D, HK * D
+    g = torch.Generator().manual_seed(3)
+    y0 = torch.randn(T, nq + 2 * nk, generator=g).to(torch.bfloat16).cuda()
+    qd0 = torch.randn(T, nq, generator=g).to(torch.bfloat16).cuda() if with_delta else None
+    pos = torch.randint(0, 900, (T,), generator=g).cuda()
+    inv = default_inv_freq(D, 1e6, "cuda")
+    dq_o = torch.randn(1, T, HQ, D, generator=g).to(torch.bfloat16).cuda()
+    dk_o = torch.randn(1, T, HK, D, generator=g).to(torch.bfloat16).cuda()
+    dv_o = torch.randn(T, nk, generator=g).to(torch.bfloat16).cuda()
+
+    def run(fused):
+        y = y0.clone().requires_grad_()
+        qd = None if qd0 is None else qd0.clone().requires_grad_()
+        if fused:
+            qo, ko, v = packed._QKVRope.apply(y, nq, nk, D, pos, inv, qd)
+        else:
+            q, k, v = y.split([nq, nk, nk], dim=-1)
+            qo, ko = rope(q.view(T, HQ, D), k.view(T, HK, D), pos, inv,
+                          q_delta=None if qd is None else qd.view(T, HQ, D))
+            qo, ko, v = qo.unsqueeze(0), ko.unsqueeze(0), v.contiguous()
+        outs, grads = [qo, ko] + ([v] if v_grad else []), [dq_o, dk_o] + ([dv_o] if v_grad else [])
+        got = torch.autograd.grad(outs, [y] + ([qd] if qd is not None else []), grads)
+        return [t.detach() for t in (qo, ko, v)] + list(got)
+
+    for a, b in zip(run(True), run(False)):
+        assert torch.equal(a, b)
