@@ -310,8 +310,30 @@ def _linear_multi(x2, bases):
     if dt != x2.dtype:
         return _fallback("fused q/k/v", f"x {x2.dtype} against compute dtype {dt}")
     w = torch.cat(ws).to(dt)
-    b = None if bs[0] is None else torch.cat(bs).to(dt)
+    if bs[0] is None:
+        b = None
+    elif any(t.requires_grad for t in bs):
+        b = torch.cat(bs).to(dt)  # gradients reach each bias
+    else:
+        b = _frozen_bias_cat(bases, bs, dt)
     return F.linear(x2, w, b)
+
+
+def _frozen_bias_cat(bases, bs, dt):
+    """The concatenation of frozen biases in dtype dt, kept on the first layer and rebuilt when
+    a bias is replaced, re-pointed or changed in place (identity, data pointer and version of
+    each; the NF4 path caches its bias_cat the same way, reference nf4/__init__.py:165-226):
+    two launches per layer and forward less for a few KB."""
+    stamp = [(t.data_ptr(), t._version) for t in bs]
+    cache = bases[0].__dict__.setdefault("_esep_bias_cat", {})
+    slot = tuple(id(m) for m in bases)
+    hit = cache.get(slot)
+    fresh = (hit is not None and hit[0] == dt and len(hit[1]) == len(bs)
+             and all(a is t for a, t in zip(hit[1], bs)) and hit[2] == stamp)
+    if not fresh:
+        with torch.no_grad():
+            hit = cache[slot] = (dt, list(bs), stamp, torch.cat(bs).to(dt))
+    return hit[3]
 
 
 def _rope_kernel_ok(rope_in, q, q_delta):
@@ -378,7 +400,7 @@ def _qkv(attn, x_q, x_ql, x_vl, rope_in):
     its own: NF4 bases through nf4.linear4bit_multi (one dequant launch into W_cat, one GEMM;
     backward one re-dequant and one dX GEMM; reference packed.py:321-352), plain nn.Linear
     bases (or plain layers themselves, FUSE_QKV) through _linear_multi. Else None (the separate
-    calls run). The fused plain output goes through _QKVRope when the RoPE kernel takes it
+    calls run). The fused output goes through _QKVRope when the RoPE kernel takes it
     (rotated True: q and k come back rotated, q's LoRA term added inside); otherwise q, k, v
     are column views of the one output (rotated False). v's LoRA term is added out of place.
     The norm backward then gets one base gradient (through x_q) beside the q and v LoRA
@@ -390,9 +412,9 @@ def _qkv(attn, x_q, x_ql, x_vl, rope_in):
     bases = [r[0] for r in routes]
     x2 = x_q.reshape(-1, x_q.shape[-1])
     n_tok = x2.shape[0]
-    y = None
     if all(nf4.is_linear4bit(b) for b in bases):
-        q, k, v = nf4.linear4bit_multi(x2, bases)
+        y = nf4.linear4bit_multi(x2, bases, split=False)
+        sizes = [b.weight.quant_state.shape[0] for b in bases]
     elif FUSE_QKV and all(type(b) is torch.nn.Linear for b in bases):
         y = _linear_multi(x2, bases)
         if y is None:
@@ -405,12 +427,12 @@ def _qkv(attn, x_q, x_ql, x_vl, rope_in):
     q_term = None
     if routes[0][1] is not None:
         q_term = LoRADeltaFunction.apply(x_ql.reshape(-1, x_ql.shape[-1]), *routes[0][1])
-    rotated = y is not None and _rope_kernel_ok(rope_in, y, q_term)
+    rotated = _rope_kernel_ok(rope_in, y, q_term)
     if rotated:
         q, k, v = _QKVRope.apply(y, sizes[0], sizes[1], attn.head_dim, rope_in.positions,
                                  rope_in.inv_freq, q_term)
         q_term = None  # added inside the kernel
-    elif y is not None:
+    else:
         q, k, v = y.split(sizes, dim=-1)
     if q_term is not None:
         q_term = q_term.view(1, n_tok, -1)

@@ -322,3 +322,35 @@ def test_qkv_rope_matches_split(with_delta, v_grad):
 
     for a, b in zip(run(True), run(False)):
         assert torch.equal(a, b)
+
+
+def test_frozen_bias_cat_cache():
+    """The fused projection's concatenation of frozen biases is built once and reused, rebuilt
+    after an in-place change of a bias (its version), a replaced bias Parameter or another
+    dtype, and never used for a bias that trains (the concatenation is then differentiable)."""
+    from solution.body import packed
+
+    lins = [torch.nn.Linear(16, n).cuda() for n in (32, 8, 8)]
+    for lin in lins:
+        lin.requires_grad_(False)
+    bs = [lin.bias for lin in lins]
+    first = packed._frozen_bias_cat(lins, bs, torch.bfloat16)
+    assert torch.equal(first, torch.cat(bs).to(torch.bfloat16))
+    assert packed._frozen_bias_cat(lins, bs, torch.bfloat16) is first
+    with torch.no_grad():
+        lins[1].bias.add_(1.0)
+    second = packed._frozen_bias_cat(lins, [lin.bias for lin in lins], torch.bfloat16)
+    assert second is not first and torch.equal(second, torch.cat(
+        [lin.bias for lin in lins]).to(torch.bfloat16))
+    lins[2].bias = torch.nn.Parameter(torch.full((8,), 3.0, device="cuda"), requires_grad=False)
+    third = packed._frozen_bias_cat(lins, [lin.bias for lin in lins], torch.bfloat16)
+    assert third is not second and torch.equal(third[-8:], torch.full((8,), 3.0, device="cuda",
+                                                                       dtype=torch.bfloat16))
+    assert packed._frozen_bias_cat(lins, [lin.bias for lin in lins], torch.float16).dtype \
+        == torch.float16
+    # a trainable bias: _linear_multi concatenates per call, with gradients to each bias
+    lins[0].bias.requires_grad_(True)
+    x = torch.randn(5, 16, device="cuda")
+    y = packed._linear_multi(x, lins)
+    y.sum().backward()
+    assert torch.equal(lins[0].bias.grad, torch.full((32,), 5.0, device="cuda"))
