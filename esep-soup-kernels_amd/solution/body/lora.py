@@ -113,6 +113,15 @@ def _rows(t, dtype):
     return flat.to(dtype).contiguous() if flat.dtype != dtype else flat.contiguous()
 
 
+def _rows_mm(t, dtype):
+    """t [..., k] as a [rows, k] matrix of dtype for torch's products, which take a row stride:
+    a 2-D view with unit column stride (such as a column block of a wider gradient) is used as
+    it is, anything else as _rows gives it."""
+    if t.dim() == 2 and t.dtype == dtype and t.stride(1) == 1 and t.stride(0) >= t.shape[1]:
+        return t
+    return _rows(t, dtype)
+
+
 class _LoRATerm:
     """The parts both Functions share: set up the forward (compute dtype, casts, key, xa) and
     turn the term's gradient into (dx, dA, dB) in the dtypes autograd expects."""
@@ -133,7 +142,7 @@ class _LoRATerm:
     @staticmethod
     def grads(ctx, dterm, x_index, a_index):
         x2, xa, a16, b16, key = ctx.saved_tensors
-        dxa, db = lora_up_bwd(_rows(dterm, ctx.dtype), xa, b16, ctx.scaling)
+        dxa, db = lora_up_bwd(_rows_mm(dterm, ctx.dtype), xa, b16, ctx.scaling)
         dx, da = lora_down_bwd(x2, a16, dxa, key, ctx.p, need_dx=ctx.needs_input_grad[x_index])
         need = ctx.needs_input_grad
         return (dx.view(ctx.x_shape).to(ctx.x_dtype) if dx is not None else None,
