@@ -180,3 +180,30 @@ def test_can_defer_without_engine_internals(monkeypatch):
     assert _can_defer_inside_backward(nr) is False
     assert nr._defer(None, torch.empty(1, 8)) is False
     assert not nr._deferred
+
+
+def test_bitsandbytes_looked_up_once(monkeypatch):
+    """is_linear4bit, which the packed decoder asks ten times per layer, looks bitsandbytes up
+    once per process: Python remembers no failed import, and a search of sys.path per call
+    made the patched forward launch-bound."""
+    import builtins
+
+    from solution import nf4
+
+    tries = []
+    real_import = builtins.__import__
+
+    def counting(name, *args, **kwargs):
+        if name.startswith("bitsandbytes"):
+            tries.append(name)
+        return real_import(name, *args, **kwargs)
+
+    nf4._bnb_class.cache_clear()
+    monkeypatch.setattr(builtins, "__import__", counting)
+    try:
+        for _ in range(5):
+            assert nf4.is_linear4bit(torch.nn.Linear(4, 4)) is False
+    finally:
+        monkeypatch.undo()
+        nf4._bnb_class.cache_clear()
+    assert len(tries) <= 1, tries
